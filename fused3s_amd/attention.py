@@ -1,0 +1,74 @@
+"""The fused SDDMM -> online softmax -> SpMM pass (f3s_1tb1rw_kernel's
+counterpart, src/fused3s_v2.cu:81-246), through the C-ABI."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from .device import DeviceArray, Stream, check
+from .graph import DeviceBSF
+
+
+def attention_fwd(Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray, bsf: DeviceBSF,
+                  window_order: DeviceArray | None = None, masked: bool = True, H: int = 1,
+                  d: int = 64, scale: float = 1.0, stream: Stream | None = None) -> None:
+    """One fused pass with each window handled whole (the reference's launch,
+    tests/test_fused_3s_v2.cu:124-131).  masked=False gives the reference's
+    tile-dense semantics."""
+    mask = bsf.tile_mask.ptr if (masked and bsf.tile_mask is not None) else None
+    if masked and mask is None:
+        raise ValueError("masked attention needs a BSF converted with masks")
+    check(_lib.hip().f3s_attention_fwd(Q.ptr, K.ptr, V.ptr, O.ptr, bsf.window_offsets.ptr,
+                                       bsf.block_col.ptr, mask,
+                                       window_order.ptr if window_order is not None else None,
+                                       bsf.W, bsf.n, d, H, scale,
+                                       stream.handle if stream else None), "f3s_attention_fwd")
+
+
+class Plan:
+    """f3s_plan: segments of heavy windows merged inside the launch."""
+
+    def __init__(self, bsf: DeviceBSF, window_order: DeviceArray | None = None, H: int = 1,
+                 seg_tiles: int = 0, stream: Stream | None = None):
+        h = C.c_void_p()
+        check(_lib.hip().f3s_plan_create(bsf.window_offsets.ptr,
+                                         window_order.ptr if window_order is not None else None,
+                                         bsf.W, H, seg_tiles, stream.handle if stream else None,
+                                         C.byref(h)), "f3s_plan_create")
+        self.handle = h.value
+        self.bsf = bsf
+        self.H = H
+        ni, ns, T = C.c_int64(), C.c_int64(), C.c_int64()
+        seg = C.c_int32()
+        check(_lib.hip().f3s_plan_info(self.handle, C.byref(ni), C.byref(ns), C.byref(T),
+                                       C.byref(seg)), "f3s_plan_info")
+        self.num_items, self.num_split, self.T, self.seg_tiles = ni.value, ns.value, T.value, seg.value
+
+    def forward(self, Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray,
+                masked: bool = True, d: int = 64, scale: float = 1.0,
+                stream: Stream | None = None) -> None:
+        bsf = self.bsf
+        mask = bsf.tile_mask.ptr if (masked and bsf.tile_mask is not None) else None
+        if masked and mask is None:
+            raise ValueError("masked attention needs a BSF converted with masks")
+        check(_lib.hip().f3s_attention_fwd_planned(self.handle, Q.ptr, K.ptr, V.ptr, O.ptr,
+                                                   bsf.block_col.ptr, mask, bsf.n, d, self.H,
+                                                   scale, stream.handle if stream else None),
+              "f3s_attention_fwd_planned")
+
+    def __del__(self):
+        try:
+            if self.handle:
+                _lib.hip().f3s_plan_destroy(self.handle)
+                self.handle = None
+        except Exception:
+            pass
+
+
+def cast_f32_to_f16(x: DeviceArray, out: DeviceArray, stream: Stream | None = None) -> None:
+    """float2half_kernel (tests/test_fused_3s_v2.cu:61-64)."""
+    count = int(np.prod(x.shape))
+    check(_lib.hip().f3s_cast_f32_to_f16(x.ptr, out.ptr, count, stream.handle if stream else None),
+          "f3s_cast_f32_to_f16")

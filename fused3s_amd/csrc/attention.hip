@@ -1,0 +1,653 @@
+// attention.hip -- fused SDDMM -> online softmax -> SpMM over the 16x16
+// block-sparse row windows, written for gfx950 (wave64, MFMA 16x16x32 f16).
+//
+// Computes what f3s_1tb1rw_kernel computes (src/fused3s_v2.cu:81-246):
+// per row window, streaming over its active tiles in order, raw logits
+// S = Q.K^T (no 1/sqrt(d) unless `scale` says so), an online softmax with a
+// running max and sum, P rounded to fp16 before P.V, and a final
+// O * (sum > 0 ? 1/sum : 0) (:235-245).  Two semantics:
+//   TILE_DENSE (tile_mask == NULL): all columns < n of an active tile are
+//     attended (the reference kernel and tests/test_fused_3s_v2.cu:17-59,
+//     with padded columns excluded as on the reference CPU side);
+//   MASKED: only the edges named by the tile's row masks
+//     (baselines/cpu_baseline.cpp:16-91).
+//
+// Work decomposition (one wave = one (item, head)):
+//   An item is a row window or, in a plan, a segment of a heavy window.
+//   The wave expands its tiles into a list of attended columns ("slots"),
+//   each with a 16-bit row mask, held in a per-wave LDS ring: 64 tiles per
+//   step, one tile per lane, positions from a wave prefix sum.  Columns no
+//   row attends are never gathered (column compaction).  Slots are consumed
+//   32 at a time:
+//     S^T[32 x 16] = K_slots[32 x 64] . Q_w^T    4 MFMA 16x16x32 (K gathered
+//                                                straight into A operands)
+//     masked online softmax, row r in lanes r, r+16, r+32, r+48
+//     O^T[64 x 16] += V_slots^T . P^T            4 MFMA (V staged in LDS)
+//   Computing S^T instead of S puts each lane's logits for row r = lane%16
+//   exactly where the B operand of the P.V product needs them, and the O^T
+//   accumulator rows of a lane are also row r, so the per-row rescale
+//   (scale_fragment_by_row, src/fused3s_v2.cu:54-71) is a plain multiply by
+//   the lane's own correction: no shuffles, no LDS round trip for P.
+//   Q stays in registers in B-operand layout for the whole item.
+//
+// MFMA 16x16x32 f16 operand layout used (CDNA3/CDNA4 16x16 family): lane l
+// supplies row l%16 of A and column l%16 of B, 8 consecutive k per lane in
+// lane group l/16; C/D: lane l holds rows 4*(l/16)+v, column l%16, v=0..3.
+// The k order inside a lane group is the same for A and B, so any consistent
+// assignment of k indices to (group, element) gives the same product; the
+// code relies only on that and on the row/column/C mapping.
+#include <math.h>
+#include <stdio.h>
+
+#include <vector>
+
+#include "f3s_common.hpp"
+#include "f3s_device.hpp"
+
+namespace f3s {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 64;             // feature dim per head (FEAT_DIM_FIXED, fused3s_v2.cu:41)
+constexpr int kChunk = 32;         // attended columns per MFMA step
+constexpr int kRing = 256;         // column ring entries per wave
+constexpr int kWavesPerWG = 4;
+constexpr int kThreads = kWave * kWavesPerWG;
+constexpr int kPartialFloats = 16 * kD + 32;   // O[16][64], m[16], l[16]
+
+struct Item {
+    int32_t w, tb, te, slot;       // slot < 0: whole window, write O directly
+};
+
+struct SplitInfo {
+    int32_t w, first_slot, nseg, pad;
+};
+
+struct __align__(16) WaveLds {
+    int32_t col[kRing];
+    uint16_t rm[kRing];
+    _Float16 v[kChunk * kD];
+};
+
+__device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Slot order of the 8 logits a lane holds (lane group g): S^T tile 0 rows
+// 4g..4g+3, then tile 1 rows 16+4g..16+4g+3.  Used as the k order of P.V.
+__device__ __forceinline__ int slot_of(int g, int j) { return (j < 4) ? 4 * g + j : 16 + 4 * g + (j - 4); }
+
+template <int H, bool MASKED>
+__global__ void __launch_bounds__(kThreads)
+fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
+                       const _Float16* __restrict__ V, float* __restrict__ O,
+                       const int32_t* __restrict__ window_offsets,
+                       const int32_t* __restrict__ block_col,
+                       const uint16_t* __restrict__ tile_mask,
+                       const int32_t* __restrict__ window_order,
+                       const Item* __restrict__ items, int64_t num_items, int32_t W, int32_t n,
+                       float scale_log2, float* __restrict__ partials,
+                       int32_t* __restrict__ counters, const SplitInfo* __restrict__ splits,
+                       const int32_t* __restrict__ slot_split)
+{
+    __shared__ WaveLds lds_all[kWavesPerWG];
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int g = lane >> 4;     // lane group
+    const int r = lane & 15;     // row of the window this lane owns (and MFMA column)
+    WaveLds& L = lds_all[wave];
+
+    const int64_t gw = (int64_t)blockIdx.x * kWavesPerWG + wave;
+    const int64_t item_idx = gw / H;
+    const int h = (int)(gw % H);
+    if (item_idx >= num_items) return;
+
+    // ---- item decode (wave-uniform) ----
+    int32_t w, tb, te, slot;
+    if (items) {
+        const Item it = items[item_idx];
+        w = it.w;
+        tb = it.tb;
+        te = it.te;
+        slot = it.slot;
+    } else {
+        w = window_order ? window_order[item_idx] : (int32_t)item_idx;
+        if (w < 0 || w >= W) return;
+        tb = window_offsets[w];
+        te = window_offsets[w + 1];
+        slot = -1;
+        const int32_t T = window_offsets[W];
+        tb = max(0, min(tb, T));
+        te = max(tb, min(te, T));
+    }
+    const int32_t nbc = (n + 15) >> 4;   // valid block columns
+
+    // ---- Q tile in registers, B-operand layout ----
+    const int32_t qrow = w * 16 + r;
+    h8 q0 = {}, q1 = {};
+    if (qrow < n) {
+        const _Float16* qp = Q + ((int64_t)qrow * H + h) * kD;
+        q0 = *reinterpret_cast<const h8*>(qp + 8 * g);
+        q1 = *reinterpret_cast<const h8*>(qp + 32 + 8 * g);
+    }
+
+    float m = -INFINITY;   // running max of row r (log2 domain)
+    float l = 0.f;         // this lane's share of the running sum of row r
+    f4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f},
+                 {0.f, 0.f, 0.f, 0.f}};
+
+    int32_t tcur = tb;
+    int32_t head = 0, tail = 0;   // ring positions (monotone)
+    constexpr int32_t kMask = kRing - 1;
+
+    while (true) {
+        // ---- expand tiles into attended columns until a chunk is ready ----
+        while (tail - head < kChunk && tcur < te) {
+            const int32_t t = tcur + lane;
+            uint32_t u = 0;
+            int32_t bc = 0;
+            uint4 mlo = make_uint4(0, 0, 0, 0), mhi = make_uint4(0, 0, 0, 0);
+            if (t < te) {
+                bc = block_col[t];
+                if (bc >= 0 && bc < nbc) {
+                    const int32_t left = n - bc * 16;
+                    const uint32_t valid = left >= 16 ? 0xffffu : ((1u << left) - 1u);
+                    if (MASKED) {
+                        const uint4* mp = reinterpret_cast<const uint4*>(tile_mask + (int64_t)t * 16);
+                        mlo = mp[0];
+                        mhi = mp[1];
+                        uint32_t o = mlo.x | mlo.y | mlo.z | mlo.w | mhi.x | mhi.y | mhi.z | mhi.w;
+                        u = (o | (o >> 16)) & valid;
+                    } else {
+                        u = valid;
+                    }
+                }
+            }
+            const int occ = __popc(u);
+            const int incl = wave_inclusive_scan(occ);
+            const int avail = kRing - (tail - head);
+            const bool accept = (t < te) && incl <= avail;
+            const uint64_t bal = __ballot(accept);
+            const int nacc = __popcll(bal);
+            const int added = __shfl(incl, nacc - 1, kWave);
+            if (accept && occ) {
+                int32_t pos = tail + incl - occ;
+                const uint32_t words[8] = {mlo.x, mlo.y, mlo.z, mlo.w, mhi.x, mhi.y, mhi.z, mhi.w};
+                uint32_t rest = u;
+                while (rest) {
+                    const int c = __ffs(rest) - 1;
+                    rest &= rest - 1;
+                    uint32_t rmask = 0xffffu;
+                    if (MASKED) {
+                        rmask = 0;
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) {
+                            rmask |= ((words[k] >> c) & 1u) << (2 * k);
+                            rmask |= ((words[k] >> (16 + c)) & 1u) << (2 * k + 1);
+                        }
+                    }
+                    L.col[pos & kMask] = bc * 16 + c;
+                    L.rm[pos & kMask] = (uint16_t)rmask;
+                    ++pos;
+                }
+            }
+            tail += added;
+            tcur += nacc;
+        }
+        const int32_t pending = tail - head;
+        if (pending <= 0) break;
+        const int cnt = pending < kChunk ? pending : kChunk;
+        F3S_WAVE_LDS_SYNC();
+
+        // ---- gather K (A operands) and V (for LDS) of this chunk ----
+        const int32_t pad_col = L.col[head & kMask];
+        const int32_t c0 = (r < cnt) ? L.col[(head + r) & kMask] : pad_col;
+        const int32_t c1 = (16 + r < cnt) ? L.col[(head + 16 + r) & kMask] : pad_col;
+        const _Float16* k0p = K + ((int64_t)c0 * H + h) * kD;
+        const _Float16* k1p = K + ((int64_t)c1 * H + h) * kD;
+        const h8 ka0 = *reinterpret_cast<const h8*>(k0p + 8 * g);
+        const h8 ka1 = *reinterpret_cast<const h8*>(k0p + 32 + 8 * g);
+        const h8 kb0 = *reinterpret_cast<const h8*>(k1p + 8 * g);
+        const h8 kb1 = *reinterpret_cast<const h8*>(k1p + 32 + 8 * g);
+        h8 vrow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int s = (lane >> 3) + 8 * i;
+            const int32_t cv = (s < cnt) ? L.col[(head + s) & kMask] : pad_col;
+            vrow[i] = *reinterpret_cast<const h8*>(V + ((int64_t)cv * H + h) * kD + 8 * (lane & 7));
+        }
+        uint32_t rmv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int s = slot_of(g, j);
+            rmv[j] = (s < cnt) ? (uint32_t)L.rm[(head + s) & kMask] : 0u;
+        }
+
+        // ---- S^T = K . Q^T ----
+        f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+        s0 = mfma16x16x32(ka0, q0, s0);
+        s0 = mfma16x16x32(ka1, q1, s0);
+        s1 = mfma16x16x32(kb0, q0, s1);
+        s1 = mfma16x16x32(kb1, q1, s1);
+
+        // ---- masked online softmax for row r ----
+        float x[8];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            x[v] = ((rmv[v] >> r) & 1u) ? s0[v] * scale_log2 : -INFINITY;
+            x[4 + v] = ((rmv[4 + v] >> r) & 1u) ? s1[v] * scale_log2 : -INFINITY;
+        }
+        float cm = x[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) cm = __builtin_fmaxf(cm, x[j]);
+        cm = __builtin_fmaxf(cm, __shfl_xor(cm, 16, kWave));
+        cm = __builtin_fmaxf(cm, __shfl_xor(cm, 32, kWave));
+        const float mn = __builtin_fmaxf(m, cm);
+        const float mu = (mn == -INFINITY) ? 0.f : mn;
+        const float corr = fast_exp2(m - mu);
+        h8 pb;
+        float ls = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const _Float16 p = (_Float16)fast_exp2(x[j] - mu);
+            pb[j] = p;
+            ls += (float)p;   // the sum uses the rounded weights P.V uses
+        }
+        l = l * corr + ls;
+        m = mn;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] *= corr;
+
+        // ---- V through LDS, transposed into A operands ----
+        F3S_WAVE_LDS_SYNC();   // previous chunk's V reads are complete
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int s = (lane >> 3) + 8 * i;
+            *reinterpret_cast<h8*>(&L.v[s * kD + 8 * (lane & 7)]) = vrow[i];
+        }
+        F3S_WAVE_LDS_SYNC();
+        h8 va[4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const h4 q = *reinterpret_cast<const h4*>(&L.v[slot_of(g, j) * kD + 4 * r]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) va[t][j] = q[t];
+        }
+        // O^T rows for tile t are dims 4*i + t (i = A row): lane (g, r) ends up
+        // holding dims 16g + 4v + t of row r.
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16x16x32(va[t], pb, acc[t]);
+
+        head += cnt;
+    }
+
+    // ---- epilogue ----
+    const int32_t orow = w * 16 + r;
+    float lrow = l + __shfl_xor(l, 16, kWave);
+    lrow += __shfl_xor(lrow, 32, kWave);
+    if (slot < 0) {
+        const float inv = lrow > 0.f ? 1.0f / lrow : 0.f;
+        if (orow < n) {
+            float* op = O + ((int64_t)orow * H + h) * kD + 16 * g;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                float4 o4 = make_float4(acc[0][v] * inv, acc[1][v] * inv, acc[2][v] * inv,
+                                        acc[3][v] * inv);
+                *reinterpret_cast<float4*>(op + 4 * v) = o4;
+            }
+        }
+        return;
+    }
+
+    // Segment of a split window: publish (m, l, O) and let the last segment
+    // of this (window, head) merge all of them in slot order.
+    float* part = partials + ((int64_t)slot * H + h) * kPartialFloats;
+    {
+        float* op = part + r * kD + 16 * g;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            *reinterpret_cast<float4*>(op + 4 * v) =
+                make_float4(acc[0][v], acc[1][v], acc[2][v], acc[3][v]);
+        if (g == 0) {
+            part[16 * kD + r] = m;
+            part[16 * kD + 16 + r] = lrow;
+        }
+    }
+    __threadfence();
+    const int32_t sid = slot_split[slot];
+    const SplitInfo si = splits[sid];
+    int32_t old = 0;
+    if (lane == 0) old = atomicAdd(&counters[(int64_t)sid * H + h], 1);
+    old = __shfl(old, 0, kWave);
+    if (old != si.nseg - 1) return;
+    __threadfence();
+
+    float M = -INFINITY;
+    for (int k = 0; k < si.nseg; ++k) {
+        const float* pk = partials + ((int64_t)(si.first_slot + k) * H + h) * kPartialFloats;
+        M = __builtin_fmaxf(M, pk[16 * kD + r]);
+    }
+    float Ls = 0.f;
+    float4 o[4] = {make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0),
+                   make_float4(0, 0, 0, 0)};
+    if (M != -INFINITY) {
+        for (int k = 0; k < si.nseg; ++k) {
+            const float* pk = partials + ((int64_t)(si.first_slot + k) * H + h) * kPartialFloats;
+            const float mk = pk[16 * kD + r];
+            const float f = fast_exp2(mk - M);
+            Ls += pk[16 * kD + 16 + r] * f;
+            const float* op = pk + r * kD + 16 * g;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                float4 a = *reinterpret_cast<const float4*>(op + 4 * v);
+                o[v].x += a.x * f;
+                o[v].y += a.y * f;
+                o[v].z += a.z * f;
+                o[v].w += a.w * f;
+            }
+        }
+    }
+    const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+    const int32_t mrow = si.w * 16 + r;
+    if (mrow < n) {
+        float* op = O + ((int64_t)mrow * H + h) * kD + 16 * g;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            *reinterpret_cast<float4*>(op + 4 * v) =
+                make_float4(o[v].x * inv, o[v].y * inv, o[v].z * inv, o[v].w * inv);
+    }
+    if (lane == 0) counters[(int64_t)sid * H + h] = 0;   // ready for the next launch
+}
+
+// ----------------------------------------------------------------- planner
+
+__global__ void plan_count(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
+                           int32_t W, int32_t seg, int32_t* __restrict__ nitems,
+                           int32_t* __restrict__ nslots, int32_t* __restrict__ nsplit)
+{
+    const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
+    if (L >= W) return;
+    const int32_t w = order ? order[L] : L;
+    int32_t ns = 1;
+    if (w >= 0 && w < W) {
+        const int32_t T = offs[W];
+        const int32_t tb = max(0, min(offs[w], T)), te = max(tb, min(offs[w + 1], T));
+        const int32_t nt = te - tb;
+        if (nt > seg) ns = (nt + seg - 1) / seg;
+    }
+    nitems[L] = ns;
+    nslots[L] = ns > 1 ? ns : 0;
+    nsplit[L] = ns > 1 ? 1 : 0;
+}
+
+__global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
+                          int32_t W, int32_t seg, const int64_t* __restrict__ item_base,
+                          const int64_t* __restrict__ slot_base,
+                          const int64_t* __restrict__ split_base, Item* __restrict__ items,
+                          SplitInfo* __restrict__ splits, int32_t* __restrict__ slot_split)
+{
+    const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
+    if (L >= W) return;
+    const int32_t w = order ? order[L] : L;
+    const int64_t ib = item_base[L];
+    const int32_t ns = (int32_t)(item_base[L + 1] - ib);
+    if (w < 0 || w >= W) {
+        items[ib] = Item{0, 0, 0, -1};   // empty item for an invalid order entry
+        return;
+    }
+    const int32_t T = offs[W];
+    const int32_t tb = max(0, min(offs[w], T)), te = max(tb, min(offs[w + 1], T));
+    if (ns == 1) {
+        items[ib] = Item{w, tb, te, -1};
+        return;
+    }
+    const int32_t sb = (int32_t)slot_base[L];
+    const int32_t sid = (int32_t)split_base[L];
+    splits[sid] = SplitInfo{w, sb, ns, 0};
+    for (int32_t k = 0; k < ns; ++k) {
+        const int32_t a = tb + k * seg;
+        const int32_t b = min(te, a + seg);
+        items[ib + k] = Item{w, a, b, sb + k};
+        slot_split[sb + k] = sid;
+    }
+}
+
+}  // namespace f3s
+
+struct f3s_plan {
+    int32_t W = 0, H = 1, seg = 0;
+    int64_t T = 0, num_items = 0, num_split = 0, num_slots = 0;
+    f3s::DeviceBuffer items, splits, slot_split, partials, counters;
+};
+
+namespace f3s {
+
+static f3s_status check_attention_args(const void* Q, const void* K, const void* V, const void* O,
+                                       int32_t n, int32_t d, int32_t H)
+{
+    F3S_REQUIRE(n >= 0, "attention: negative n");
+    if (d != kD) {
+        set_error("attention: only d == 64 is implemented (FEAT_DIM_FIXED of the reference)");
+        return F3S_EUNSUPPORTED;
+    }
+    if (H != 1 && H != 2 && H != 4) {
+        set_error("attention: H must be 1, 2 or 4");
+        return F3S_EUNSUPPORTED;
+    }
+    F3S_REQUIRE(n == 0 || (Q && K && V && O), "attention: NULL feature pointer");
+    F3S_REQUIRE(((((uintptr_t)Q) | ((uintptr_t)K) | ((uintptr_t)V) | ((uintptr_t)O)) & 15) == 0,
+                "attention: Q, K, V, O must be 16-byte aligned");
+    return F3S_OK;
+}
+
+template <int H>
+static void launch_h(bool masked, dim3 grid, hipStream_t st, const _Float16* Q, const _Float16* K,
+                     const _Float16* V, float* O, const int32_t* offs, const int32_t* bcol,
+                     const uint16_t* mask, const int32_t* order, const Item* items,
+                     int64_t num_items, int32_t W, int32_t n, float sl2, float* partials,
+                     int32_t* counters, const SplitInfo* splits, const int32_t* slot_split)
+{
+    if (masked)
+        hipLaunchKernelGGL((fused_attention_kernel<H, true>), grid, dim3(kThreads), 0, st, Q, K,
+                           V, O, offs, bcol, mask, order, items, num_items, W, n, sl2, partials,
+                           counters, splits, slot_split);
+    else
+        hipLaunchKernelGGL((fused_attention_kernel<H, false>), grid, dim3(kThreads), 0, st, Q, K,
+                           V, O, offs, bcol, mask, order, items, num_items, W, n, sl2, partials,
+                           counters, splits, slot_split);
+}
+
+static f3s_status launch(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,
+                         const int32_t* offs, const int32_t* bcol, const uint16_t* mask,
+                         const int32_t* order, const Item* items, int64_t num_items, int32_t W,
+                         int32_t n, int32_t H, float scale, float* partials, int32_t* counters,
+                         const SplitInfo* splits, const int32_t* slot_split, hipStream_t st)
+{
+    if (num_items <= 0) return F3S_OK;
+    const int64_t waves = num_items * H;
+    const int64_t blocks = ceil_div(waves, kWavesPerWG);
+    F3S_REQUIRE(blocks < ((int64_t)1 << 31), "attention: too many work items");
+    const float sl2 = scale * 1.4426950408889634f;
+    const dim3 grid((unsigned)blocks);
+    auto q = reinterpret_cast<const _Float16*>(Q);
+    auto k = reinterpret_cast<const _Float16*>(K);
+    auto v = reinterpret_cast<const _Float16*>(V);
+    const bool masked = mask != nullptr;
+    if (H == 1)
+        launch_h<1>(masked, grid, st, q, k, v, O, offs, bcol, mask, order, items, num_items, W,
+                    n, sl2, partials, counters, splits, slot_split);
+    else if (H == 2)
+        launch_h<2>(masked, grid, st, q, k, v, O, offs, bcol, mask, order, items, num_items, W,
+                    n, sl2, partials, counters, splits, slot_split);
+    else
+        launch_h<4>(masked, grid, st, q, k, v, O, offs, bcol, mask, order, items, num_items, W,
+                    n, sl2, partials, counters, splits, slot_split);
+    F3S_HIP(hipGetLastError());
+    return F3S_OK;
+}
+
+}  // namespace f3s
+
+using namespace f3s;
+
+extern "C" {
+
+f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,
+                             const int32_t* d_window_offsets, const int32_t* d_block_col,
+                             const uint16_t* d_tile_mask, const int32_t* d_window_order,
+                             int32_t W, int32_t n, int32_t d, int32_t H, float scale,
+                             void* stream)
+{
+    F3S_TRY(check_attention_args(Q, K, V, O, n, d, H));
+    F3S_REQUIRE(W == (int32_t)ceil_div(n, 16), "f3s_attention_fwd: W must equal ceil(n/16)");
+    F3S_REQUIRE(W == 0 || (d_window_offsets && d_block_col),
+                "f3s_attention_fwd: NULL block-sparse pointer");
+    F3S_REQUIRE((((uintptr_t)d_tile_mask) & 15) == 0, "f3s_attention_fwd: tile_mask alignment");
+    F3S_TRY(require_device());
+    clear_error();
+    return launch(Q, K, V, O, d_window_offsets, d_block_col, d_tile_mask, d_window_order, nullptr,
+                  W, W, n, H, scale, nullptr, nullptr, nullptr, nullptr, as_stream(stream));
+}
+
+f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_window_order,
+                           int32_t W, int32_t H, int32_t seg_tiles, void* stream,
+                           f3s_plan** plan_out)
+{
+    F3S_REQUIRE(plan_out != nullptr, "f3s_plan_create: NULL out pointer");
+    *plan_out = nullptr;
+    F3S_REQUIRE(W >= 0, "f3s_plan_create: negative W");
+    F3S_REQUIRE(W == 0 || d_window_offsets, "f3s_plan_create: NULL window_offsets");
+    F3S_REQUIRE(H == 1 || H == 2 || H == 4, "f3s_plan_create: H must be 1, 2 or 4");
+    F3S_REQUIRE(seg_tiles >= 0, "f3s_plan_create: negative seg_tiles");
+    F3S_TRY(require_device());
+    clear_error();
+    hipStream_t st = as_stream(stream);
+
+    f3s_plan* p = new f3s_plan();
+    p->W = W;
+    p->H = H;
+    int32_t T32 = 0;
+    if (W > 0) {
+        F3S_HIP(hipMemcpyAsync(&T32, d_window_offsets + W, sizeof T32, hipMemcpyDeviceToHost, st));
+        F3S_HIP(hipStreamSynchronize(st));
+    }
+    p->T = T32;
+    // Automatic segment size: enough segments that the heaviest item is a
+    // small fraction of one wave slot's share of the whole pass.
+    int64_t seg = seg_tiles;
+    if (seg == 0) {
+        seg = ceil_div(p->T * H, 8192);
+        if (seg < 64) seg = 64;
+    }
+    if (seg > INT32_MAX) seg = INT32_MAX;
+    p->seg = (int32_t)seg;
+
+    DeviceBuffer cnt_items, cnt_slots, cnt_split, base_items, base_slots, base_split, tmp;
+    auto fail = [&](f3s_status s) {
+        delete p;
+        return s;
+    };
+    f3s_status s;
+    if ((s = cnt_items.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
+        (s = cnt_slots.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
+        (s = cnt_split.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
+        (s = base_items.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
+        (s = base_slots.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
+        (s = base_split.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
+        (s = tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(W))) != F3S_OK)
+        return fail(s);
+    auto* ci = reinterpret_cast<int32_t*>(cnt_items.ptr);
+    auto* cs = reinterpret_cast<int32_t*>(cnt_slots.ptr);
+    auto* cp = reinterpret_cast<int32_t*>(cnt_split.ptr);
+    auto* bi = reinterpret_cast<int64_t*>(base_items.ptr);
+    auto* bs = reinterpret_cast<int64_t*>(base_slots.ptr);
+    auto* bp = reinterpret_cast<int64_t*>(base_split.ptr);
+    if (W > 0) {
+        hipLaunchKernelGGL(plan_count, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
+                           d_window_offsets, d_window_order, W, p->seg, ci, cs, cp);
+        if (hipGetLastError() != hipSuccess) return fail(F3S_EHIP);
+    }
+    auto* tp = reinterpret_cast<int64_t*>(tmp.ptr);
+    if ((s = exclusive_scan_i32_to_i64(ci, bi, W, tp, st)) != F3S_OK ||
+        (s = exclusive_scan_i32_to_i64(cs, bs, W, tp, st)) != F3S_OK ||
+        (s = exclusive_scan_i32_to_i64(cp, bp, W, tp, st)) != F3S_OK)
+        return fail(s);
+    int64_t totals[3] = {0, 0, 0};
+    if (hipMemcpyAsync(&totals[0], bi + W, 8, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipMemcpyAsync(&totals[1], bs + W, 8, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipMemcpyAsync(&totals[2], bp + W, 8, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return fail(hip_fail(hipGetLastError(), "plan totals", __FILE__, __LINE__));
+    p->num_items = totals[0];
+    p->num_slots = totals[1];
+    p->num_split = totals[2];
+    if ((s = p->items.reserve(sizeof(Item) * (size_t)(p->num_items + 1))) != F3S_OK ||
+        (s = p->splits.reserve(sizeof(SplitInfo) * (size_t)(p->num_split + 1))) != F3S_OK ||
+        (s = p->slot_split.reserve(sizeof(int32_t) * (size_t)(p->num_slots + 1))) != F3S_OK ||
+        (s = p->partials.reserve(sizeof(float) * (size_t)kPartialFloats * H *
+                                 (size_t)(p->num_slots + 1))) != F3S_OK ||
+        (s = p->counters.reserve(sizeof(int32_t) * (size_t)H * (size_t)(p->num_split + 1))) !=
+            F3S_OK)
+        return fail(s);
+    if (hipMemsetAsync(p->counters.ptr, 0, p->counters.bytes, st) != hipSuccess)
+        return fail(hip_fail(hipGetLastError(), "plan counters", __FILE__, __LINE__));
+    if (W > 0) {
+        hipLaunchKernelGGL(plan_fill, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
+                           d_window_offsets, d_window_order, W, p->seg, bi, bs, bp,
+                           reinterpret_cast<Item*>(p->items.ptr),
+                           reinterpret_cast<SplitInfo*>(p->splits.ptr),
+                           reinterpret_cast<int32_t*>(p->slot_split.ptr));
+        if (hipGetLastError() != hipSuccess) return fail(F3S_EHIP);
+    }
+    if (hipStreamSynchronize(st) != hipSuccess)
+        return fail(hip_fail(hipGetLastError(), "plan build", __FILE__, __LINE__));
+    *plan_out = p;
+    return F3S_OK;
+}
+
+f3s_status f3s_plan_destroy(f3s_plan* plan)
+{
+    delete plan;
+    return F3S_OK;
+}
+
+f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_split_windows,
+                         int64_t* T, int32_t* seg_tiles)
+{
+    F3S_REQUIRE(plan != nullptr, "f3s_plan_info: NULL plan");
+    if (num_items) *num_items = plan->num_items;
+    if (num_split_windows) *num_split_windows = plan->num_split;
+    if (T) *T = plan->T;
+    if (seg_tiles) *seg_tiles = plan->seg;
+    return F3S_OK;
+}
+
+f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, const uint16_t* K,
+                                     const uint16_t* V, float* O, const int32_t* d_block_col,
+                                     const uint16_t* d_tile_mask, int32_t n, int32_t d, int32_t H,
+                                     float scale, void* stream)
+{
+    F3S_REQUIRE(plan != nullptr, "f3s_attention_fwd_planned: NULL plan");
+    F3S_TRY(check_attention_args(Q, K, V, O, n, d, H));
+    F3S_REQUIRE(H == plan->H, "f3s_attention_fwd_planned: H differs from the plan's");
+    F3S_REQUIRE(plan->W == (int32_t)ceil_div(n, 16),
+                "f3s_attention_fwd_planned: n does not match the plan's W");
+    F3S_REQUIRE(plan->T == 0 || d_block_col, "f3s_attention_fwd_planned: NULL block_col");
+    F3S_REQUIRE((((uintptr_t)d_tile_mask) & 15) == 0,
+                "f3s_attention_fwd_planned: tile_mask alignment");
+    F3S_TRY(require_device());
+    clear_error();
+    return launch(Q, K, V, O, nullptr, d_block_col, d_tile_mask, nullptr,
+                  reinterpret_cast<const Item*>(plan->items.ptr), plan->num_items, plan->W, n, H,
+                  scale, reinterpret_cast<float*>(plan->partials.ptr),
+                  reinterpret_cast<int32_t*>(plan->counters.ptr),
+                  reinterpret_cast<const SplitInfo*>(plan->splits.ptr),
+                  reinterpret_cast<const int32_t*>(plan->slot_split.ptr), as_stream(stream));
+}
+
+}  // extern "C"

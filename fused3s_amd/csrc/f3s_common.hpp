@@ -1,0 +1,70 @@
+// f3s_common.hpp -- shared helpers of libf3s_hip.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/f3s_capi.h"
+
+namespace f3s {
+
+// Per-thread detail of the last failure (returned by f3s_last_error).
+void set_error(const std::string& msg);
+void clear_error();
+
+// Turns a HIP error into F3S_EHIP (or F3S_ENOMEM / F3S_ENODEV) and records
+// where it happened.
+f3s_status hip_fail(hipError_t err, const char* what, const char* file, int line);
+
+// Validates that a device is present and current; F3S_ENODEV otherwise.
+f3s_status require_device();
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Device-wide exclusive scan of int32 counts into int64 (or int32) prefix
+// sums; out has count + 1 entries (out[count] = total).  tmp needs
+// scan_tmp_elems(count) int64 elements.
+int64_t scan_tmp_elems(int64_t count);
+f3s_status exclusive_scan_i32_to_i64(const int32_t* in, int64_t* out, int64_t count,
+                                     int64_t* tmp, hipStream_t stream);
+
+// Small grow-only device buffer (per call site).
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    f3s_status reserve(size_t want);
+    void release();
+    ~DeviceBuffer() { release(); }
+};
+
+}  // namespace f3s
+
+#define F3S_HIP(call)                                                        \
+    do {                                                                     \
+        hipError_t f3s_err_ = (call);                                        \
+        if (f3s_err_ != hipSuccess)                                          \
+            return ::f3s::hip_fail(f3s_err_, #call, __FILE__, __LINE__);     \
+    } while (0)
+
+#define F3S_TRY(call)                                                        \
+    do {                                                                     \
+        f3s_status f3s_st_ = (call);                                         \
+        if (f3s_st_ != F3S_OK) return f3s_st_;                               \
+    } while (0)
+
+#define F3S_REQUIRE(cond, msg)                                               \
+    do {                                                                     \
+        if (!(cond)) {                                                       \
+            ::f3s::set_error(msg);                                           \
+            return F3S_EINVAL;                                               \
+        }                                                                    \
+    } while (0)
+
+// Orders this wave's LDS traffic: every LDS access issued before completes
+// before any issued after, and the compiler may not move memory operations
+// across it.  Sufficient for LDS shared between the lanes of one wave.
+#define F3S_WAVE_LDS_SYNC() asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory")

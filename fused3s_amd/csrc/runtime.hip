@@ -1,0 +1,337 @@
+// runtime.hip -- error reporting, device plumbing, fp32->fp16 cast and the
+// device-wide scan used by the converter and the planner.
+#include <stdio.h>
+
+#include <string>
+
+#include "f3s_common.hpp"
+#include "f3s_device.hpp"
+
+namespace f3s {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+f3s_status hip_fail(hipError_t err, const char* what, const char* file, int line)
+{
+    char buf[512];
+    snprintf(buf, sizeof buf, "%s failed at %s:%d: %s (%d)", what, file, line,
+             hipGetErrorString(err), (int)err);
+    set_error(buf);
+    if (err == hipErrorOutOfMemory) return F3S_ENOMEM;
+    if (err == hipErrorNoDevice || err == hipErrorInvalidDevice) return F3S_ENODEV;
+    return F3S_EHIP;
+}
+
+f3s_status require_device()
+{
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        set_error("no HIP device visible");
+        return F3S_ENODEV;
+    }
+    return F3S_OK;
+}
+
+f3s_status DeviceBuffer::reserve(size_t want)
+{
+    if (want <= bytes && ptr) return F3S_OK;
+    release();
+    size_t alloc = want ? want : 1;
+    F3S_HIP(hipMalloc(&ptr, alloc));
+    bytes = alloc;
+    return F3S_OK;
+}
+
+void DeviceBuffer::release()
+{
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+}
+
+// ------------------------------------------------------------------ scan
+
+constexpr int kScanThreads = 256;
+constexpr int kScanPerThread = 8;
+constexpr int kScanTile = kScanThreads * kScanPerThread;
+
+int64_t scan_tmp_elems(int64_t count) { return ceil_div(count, kScanTile) + 1; }
+
+__global__ void __launch_bounds__(kScanThreads)
+scan_block_sums(const int32_t* __restrict__ in, int64_t count, int64_t* __restrict__ sums)
+{
+    __shared__ int64_t lds[kScanThreads / kWave];
+    const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanPerThread;
+    int64_t s = 0;
+#pragma unroll
+    for (int i = 0; i < kScanPerThread; ++i)
+        if (base + i < count) s += in[base + i];
+    int64_t total;
+    (void)block_exclusive_scan<kScanThreads>(s, lds, total);
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+// One workgroup: exclusive scan of the block sums in place; writes the grand
+// total to *total_out.
+__global__ void __launch_bounds__(kScanThreads)
+scan_sums_single(int64_t* __restrict__ sums, int64_t nblocks, int64_t* __restrict__ total_out)
+{
+    __shared__ int64_t lds[kScanThreads / kWave];
+    int64_t carry = 0;
+    for (int64_t b0 = 0; b0 < nblocks; b0 += kScanThreads) {
+        int64_t i = b0 + threadIdx.x;
+        int64_t v = i < nblocks ? sums[i] : 0;
+        int64_t total;
+        int64_t ex = block_exclusive_scan<kScanThreads>(v, lds, total);
+        if (i < nblocks) sums[i] = carry + ex;
+        carry += total;
+    }
+    if (threadIdx.x == 0) *total_out = carry;
+}
+
+__global__ void __launch_bounds__(kScanThreads)
+scan_apply(const int32_t* __restrict__ in, int64_t count, const int64_t* __restrict__ sums,
+           int64_t* __restrict__ out)
+{
+    __shared__ int64_t lds[kScanThreads / kWave];
+    const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanPerThread;
+    int64_t v[kScanPerThread];
+    int64_t s = 0;
+#pragma unroll
+    for (int i = 0; i < kScanPerThread; ++i) {
+        v[i] = (base + i < count) ? in[base + i] : 0;
+        s += v[i];
+    }
+    int64_t total;
+    int64_t ex = block_exclusive_scan<kScanThreads>(s, lds, total) + sums[blockIdx.x];
+#pragma unroll
+    for (int i = 0; i < kScanPerThread; ++i) {
+        if (base + i < count) out[base + i] = ex;
+        ex += v[i];
+    }
+}
+
+f3s_status exclusive_scan_i32_to_i64(const int32_t* in, int64_t* out, int64_t count,
+                                     int64_t* tmp, hipStream_t stream)
+{
+    if (count <= 0) {
+        F3S_HIP(hipMemsetAsync(out, 0, sizeof(int64_t), stream));
+        return F3S_OK;
+    }
+    const int64_t nb = ceil_div(count, kScanTile);
+    hipLaunchKernelGGL(scan_block_sums, dim3((unsigned)nb), dim3(kScanThreads), 0, stream,
+                       in, count, tmp);
+    hipLaunchKernelGGL(scan_sums_single, dim3(1), dim3(kScanThreads), 0, stream, tmp, nb,
+                       out + count);
+    hipLaunchKernelGGL(scan_apply, dim3((unsigned)nb), dim3(kScanThreads), 0, stream, in,
+                       count, tmp, out);
+    F3S_HIP(hipGetLastError());
+    return F3S_OK;
+}
+
+// ------------------------------------------------------------------ cast
+
+// float2half_kernel (tests/test_fused_3s_v2.cu:61-64); 4 elements per thread,
+// v_cvt_f16_f32 rounds to nearest even.
+__global__ void __launch_bounds__(256)
+cast_f32_to_f16_kernel(const float* __restrict__ in, _Float16* __restrict__ out, int64_t count)
+{
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i + 3 < count && ((((uintptr_t)in) | ((uintptr_t)out)) & 15) == 0) {
+        float4 v = *reinterpret_cast<const float4*>(in + i);
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        h4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+        *reinterpret_cast<h4*>(out + i) = h;
+    } else {
+        for (int64_t j = i; j < i + 4 && j < count; ++j) out[j] = (_Float16)in[j];
+    }
+}
+
+}  // namespace f3s
+
+using namespace f3s;
+
+extern "C" {
+
+const char* f3s_status_string(f3s_status s)
+{
+    switch (s) {
+    case F3S_OK: return "F3S_OK";
+    case F3S_EINVAL: return "F3S_EINVAL: invalid argument";
+    case F3S_ENOMEM: return "F3S_ENOMEM: device out of memory";
+    case F3S_EHIP: return "F3S_EHIP: HIP runtime error";
+    case F3S_ENODEV: return "F3S_ENODEV: no GPU device";
+    case F3S_EUNSUPPORTED: return "F3S_EUNSUPPORTED: unsupported configuration";
+    case F3S_EDATA: return "F3S_EDATA: input violates the format";
+    default: return "F3S: unknown status";
+    }
+}
+
+const char* f3s_last_error(void) { return g_last_error.c_str(); }
+
+int32_t f3s_abi_version(void) { return F3S_ABI_VERSION; }
+
+f3s_status f3s_device_count(int32_t* count)
+{
+    F3S_REQUIRE(count != nullptr, "f3s_device_count: count is NULL");
+    int c = 0;
+    hipError_t e = hipGetDeviceCount(&c);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        c = 0;
+    }
+    *count = c;
+    return F3S_OK;
+}
+
+f3s_status f3s_set_device(int32_t device)
+{
+    F3S_TRY(require_device());
+    F3S_HIP(hipSetDevice(device));
+    return F3S_OK;
+}
+
+f3s_status f3s_device_name(char* buf, int32_t buflen)
+{
+    F3S_REQUIRE(buf != nullptr && buflen > 0, "f3s_device_name: bad buffer");
+    F3S_TRY(require_device());
+    int dev = 0;
+    F3S_HIP(hipGetDevice(&dev));
+    hipDeviceProp_t p;
+    F3S_HIP(hipGetDeviceProperties(&p, dev));
+    snprintf(buf, (size_t)buflen, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return F3S_OK;
+}
+
+f3s_status f3s_malloc(void** ptr, uint64_t bytes)
+{
+    F3S_REQUIRE(ptr != nullptr, "f3s_malloc: ptr is NULL");
+    *ptr = nullptr;
+    F3S_TRY(require_device());
+    F3S_HIP(hipMalloc(ptr, bytes ? bytes : 1));
+    return F3S_OK;
+}
+
+f3s_status f3s_free(void* ptr)
+{
+    if (!ptr) return F3S_OK;
+    F3S_HIP(hipFree(ptr));
+    return F3S_OK;
+}
+
+f3s_status f3s_memcpy_h2d(void* dst, const void* src, uint64_t bytes, void* stream)
+{
+    if (!bytes) return F3S_OK;
+    F3S_REQUIRE(dst && src, "f3s_memcpy_h2d: NULL pointer");
+    F3S_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)));
+    F3S_HIP(hipStreamSynchronize(as_stream(stream)));
+    return F3S_OK;
+}
+
+f3s_status f3s_memcpy_d2h(void* dst, const void* src, uint64_t bytes, void* stream)
+{
+    if (!bytes) return F3S_OK;
+    F3S_REQUIRE(dst && src, "f3s_memcpy_d2h: NULL pointer");
+    F3S_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)));
+    F3S_HIP(hipStreamSynchronize(as_stream(stream)));
+    return F3S_OK;
+}
+
+f3s_status f3s_memcpy_d2d(void* dst, const void* src, uint64_t bytes, void* stream)
+{
+    if (!bytes) return F3S_OK;
+    F3S_REQUIRE(dst && src, "f3s_memcpy_d2d: NULL pointer");
+    F3S_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+    return F3S_OK;
+}
+
+f3s_status f3s_memset(void* ptr, int32_t value, uint64_t bytes, void* stream)
+{
+    if (!bytes) return F3S_OK;
+    F3S_REQUIRE(ptr != nullptr, "f3s_memset: NULL pointer");
+    F3S_HIP(hipMemsetAsync(ptr, value, bytes, as_stream(stream)));
+    return F3S_OK;
+}
+
+f3s_status f3s_synchronize(void* stream)
+{
+    F3S_TRY(require_device());
+    if (stream) {
+        F3S_HIP(hipStreamSynchronize(as_stream(stream)));
+    } else {
+        F3S_HIP(hipDeviceSynchronize());
+    }
+    return F3S_OK;
+}
+
+f3s_status f3s_stream_create(void** stream)
+{
+    F3S_REQUIRE(stream != nullptr, "f3s_stream_create: NULL out pointer");
+    F3S_TRY(require_device());
+    hipStream_t s;
+    F3S_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return F3S_OK;
+}
+
+f3s_status f3s_stream_destroy(void* stream)
+{
+    if (!stream) return F3S_OK;
+    F3S_HIP(hipStreamDestroy(as_stream(stream)));
+    return F3S_OK;
+}
+
+f3s_status f3s_event_create(void** event)
+{
+    F3S_REQUIRE(event != nullptr, "f3s_event_create: NULL out pointer");
+    F3S_TRY(require_device());
+    hipEvent_t e;
+    F3S_HIP(hipEventCreate(&e));
+    *event = e;
+    return F3S_OK;
+}
+
+f3s_status f3s_event_destroy(void* event)
+{
+    if (!event) return F3S_OK;
+    F3S_HIP(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
+    return F3S_OK;
+}
+
+f3s_status f3s_event_record(void* event, void* stream)
+{
+    F3S_REQUIRE(event != nullptr, "f3s_event_record: NULL event");
+    F3S_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)));
+    return F3S_OK;
+}
+
+f3s_status f3s_event_elapsed_ms(void* start, void* stop, float* ms)
+{
+    F3S_REQUIRE(start && stop && ms, "f3s_event_elapsed_ms: NULL argument");
+    F3S_HIP(hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop)));
+    F3S_HIP(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                reinterpret_cast<hipEvent_t>(stop)));
+    return F3S_OK;
+}
+
+f3s_status f3s_cast_f32_to_f16(const float* d_in, uint16_t* d_out, int64_t count, void* stream)
+{
+    F3S_REQUIRE(count >= 0, "f3s_cast_f32_to_f16: negative count");
+    if (count == 0) return F3S_OK;
+    F3S_REQUIRE(d_in && d_out, "f3s_cast_f32_to_f16: NULL pointer");
+    F3S_TRY(require_device());
+    const int64_t threads = ceil_div(count, 4);
+    const int64_t blocks = ceil_div(threads, 256);
+    F3S_REQUIRE(blocks < (int64_t)1 << 31, "f3s_cast_f32_to_f16: count too large");
+    hipLaunchKernelGGL(cast_f32_to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       as_stream(stream), d_in, reinterpret_cast<_Float16*>(d_out), count);
+    F3S_HIP(hipGetLastError());
+    return F3S_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,60 @@
+// graph.hpp -- drop-in C++ host API of the fused3S hot path.
+//
+// Same names, argument meaning and return types as the reference's
+// include/utils.cuh:19-59 and src/converter.cu:13, so a caller of the
+// reference links libf3s_host.so instead.  Differences, all deliberate:
+//   * load_csr_graph reads col_idx.txt (the exporter's name) and throws
+//     std::runtime_error on a missing or malformed file instead of returning
+//     an all-zero graph (utils.cuh:36 opens col_ind.txt and never checks);
+//   * blockSparseFormat carries the new intra-tile row masks;
+//   * convert_csr_to_block_sparse runs on the GPU through libf3s_hip.so
+//     (bit-exact with the reference's host converter) and throws if no GPU
+//     is usable; it prints the same two lines as the reference (:42-43);
+//   * F3S_CHECK replaces CUDA_CHECK (utils.cuh:9-17) for f3s_status codes.
+#pragma once
+
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../f3s_capi.h"
+
+#define F3S_CHECK(call)                                                                  \
+    do {                                                                                 \
+        f3s_status f3s_chk_ = (call);                                                    \
+        if (f3s_chk_ != F3S_OK) {                                                        \
+            f3s_report_failure(f3s_chk_, #call, __FILE__, __LINE__);                     \
+        }                                                                                \
+    } while (0)
+
+// Prints the status, the library's detail message and the call site, then
+// exits with EXIT_FAILURE (the behaviour of CUDA_CHECK, utils.cuh:13-15).
+[[noreturn]] void f3s_report_failure(f3s_status s, const char* call, const char* file, int line);
+
+// include/utils.cuh:19-24
+struct GraphData {
+    int num_nodes = 0;
+    int num_edges = 0;
+    std::vector<int> row_ptr;
+    std::vector<int> col_ind;
+};
+
+// include/utils.cuh:26-40
+GraphData load_csr_graph(const std::string& dataset_dir);
+
+// include/utils.cuh:42-46, plus tile_masks (16 uint16 per active tile: bit c
+// of entry r <=> edge (16w + r, 16*block_col + c)).
+struct blockSparseFormat {
+    int num_row_windows = 0;
+    std::vector<int> window_offsets;
+    std::vector<int> block_col_indices;
+    std::vector<uint16_t> tile_masks;
+};
+
+// src/converter.cu:13-44
+blockSparseFormat convert_csr_to_block_sparse(int num_nodes, const std::vector<int>& row_ptr,
+                                              const std::vector<int>& col_ind);
+
+// include/utils.cuh:48-59
+std::vector<int> generate_balanced_window_order(const blockSparseFormat& format);

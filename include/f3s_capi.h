@@ -1,0 +1,140 @@
+/*
+ * f3s_capi.h -- C-ABI of libf3s_hip.so, the MI355X (gfx950) implementation of
+ * the fused3S hot path: CSR -> 16x16 block-sparse conversion, window ordering
+ * and the fused SDDMM -> online softmax -> SpMM pass.
+ *
+ * Plain C: no HIP or torch types.  Device buffers are `void*`/typed pointers
+ * obtained from f3s_malloc (or any HIP allocation in the same process);
+ * streams are `void*` (a hipStream_t, NULL = the default stream).  Every
+ * function returns f3s_status (0 = F3S_OK) and never exits the process; the
+ * detail of the last failure on the calling thread is f3s_last_error().
+ *
+ * Layouts:
+ *   CSR            row_ptr int32[n+1], col_idx int32[nnz] (columns < n)
+ *   block-sparse   W = ceil(n/16) row windows; window_offsets int32[W+1];
+ *                  block_col int32[T] (ascending per window);
+ *                  tile_mask uint16[T][16]: bit c of row r <=> edge
+ *                  (16w + r, 16*block_col + c)
+ *   features       Q, K, V: IEEE binary16 bits, node-major [n][H][d];
+ *                  O: float32 [n][H][d].  Buffers need n rows (a reference-
+ *                  style buffer padded to 16W rows also works).
+ *
+ * Thread safety: calls on different streams may run concurrently; the
+ * library keeps no mutable global state besides the per-thread last error
+ * and the per-device scratch of the planned path (documented there).
+ */
+#ifndef F3S_CAPI_H
+#define F3S_CAPI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t f3s_status;
+
+#define F3S_OK 0
+#define F3S_EINVAL 1        /* bad size, pointer or argument */
+#define F3S_ENOMEM 2        /* device allocation failed */
+#define F3S_EHIP 3          /* a HIP runtime call failed (detail in f3s_last_error) */
+#define F3S_ENODEV 4        /* no usable GPU */
+#define F3S_EUNSUPPORTED 5  /* valid but not implemented here (e.g. d != 64) */
+#define F3S_EDATA 6         /* input data violates the format (e.g. column >= n) */
+
+#define F3S_ABI_VERSION 1
+
+/* Semantics of f3s_attention_fwd*: tile_mask == NULL selects TILE_DENSE
+ * (every column < n of every active tile is attended: the reference kernel
+ * and test ground truth, tests/test_fused_3s_v2.cu:17-59); a mask selects
+ * MASKED (edge-exact, baselines/cpu_baseline.cpp:16-91). */
+
+const char* f3s_status_string(f3s_status s);
+const char* f3s_last_error(void);
+int32_t f3s_abi_version(void);
+
+/* ---- device plumbing (replaces the CUDA_CHECK'ed runtime calls of the
+ *      reference harness, tests/test_fused_3s_v2.cu:93-120,139,157-159) ---- */
+f3s_status f3s_device_count(int32_t* count);
+f3s_status f3s_set_device(int32_t device);
+f3s_status f3s_device_name(char* buf, int32_t buflen);
+f3s_status f3s_malloc(void** ptr, uint64_t bytes);
+f3s_status f3s_free(void* ptr);
+f3s_status f3s_memcpy_h2d(void* dst, const void* src, uint64_t bytes, void* stream);
+f3s_status f3s_memcpy_d2h(void* dst, const void* src, uint64_t bytes, void* stream);
+f3s_status f3s_memcpy_d2d(void* dst, const void* src, uint64_t bytes, void* stream);
+f3s_status f3s_memset(void* ptr, int32_t value, uint64_t bytes, void* stream);
+f3s_status f3s_synchronize(void* stream);            /* NULL: whole device */
+f3s_status f3s_stream_create(void** stream);
+f3s_status f3s_stream_destroy(void* stream);
+f3s_status f3s_event_create(void** event);
+f3s_status f3s_event_destroy(void* event);
+f3s_status f3s_event_record(void* event, void* stream);
+f3s_status f3s_event_elapsed_ms(void* start, void* stop, float* ms);  /* waits for stop */
+
+/* float2half_kernel (tests/test_fused_3s_v2.cu:61-64): IEEE round to
+ * nearest even, elementwise. */
+f3s_status f3s_cast_f32_to_f16(const float* d_in, uint16_t* d_out, int64_t count, void* stream);
+
+/* convert_csr_to_block_sparse (src/converter.cu:13-44), on the GPU.
+ * d_window_offsets[W+1] is always written and *T_out receives T (the call
+ * synchronises `stream` to read it).  When d_block_col is non-NULL the tile
+ * lists are written too (it must hold T entries), and when d_tile_mask is
+ * non-NULL the 16 row masks of each tile (T*16 entries).  Typical use is two
+ * calls: sizes first (d_block_col = NULL), then the lists.  Output is
+ * bit-exact with the reference converter.  F3S_EDATA if row_ptr is not
+ * monotone from 0 to nnz or a column is outside [0, n). */
+f3s_status f3s_convert_csr_to_bsf(const int32_t* d_row_ptr, const int32_t* d_col_idx,
+                                  int32_t n, int64_t nnz,
+                                  int32_t* d_window_offsets, int32_t* d_block_col,
+                                  uint16_t* d_tile_mask, int64_t* T_out, void* stream);
+
+/* generate_balanced_window_order (include/utils.cuh:48-59), on the GPU:
+ * windows by descending tile count, ties by ascending window index. */
+f3s_status f3s_window_order(const int32_t* d_window_offsets, int32_t W,
+                            int32_t* d_order, void* stream);
+
+/* Figures behind the algorithmic byte model (no reference counterpart):
+ * occ_sum = sum over tiles of the columns the fused pass gathers (popcount of
+ * the OR of the row masks if d_tile_mask, else the tile's columns < n);
+ * mask_bits = popcount of all masks.  Synchronises `stream`. */
+f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask,
+                         int64_t T, int32_t n, int64_t* occ_sum, int64_t* mask_bits,
+                         void* stream);
+
+/* f3s_1tb1rw_kernel (src/fused3s_v2.cu:81-90) and its launch
+ * (tests/test_fused_3s_v2.cu:124-131): one fused pass, each row window
+ * handled whole, windows taken in d_window_order (NULL = natural order).
+ * O[i] = sum_j softmax_j(scale * Q[i].K[j]) V[j] per head; rows with no
+ * attended column get 0.  Requires d == 64, H in {1, 2, 4}; scale = 1
+ * reproduces the reference (which has no scaling). */
+f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                             float* O, const int32_t* d_window_offsets,
+                             const int32_t* d_block_col, const uint16_t* d_tile_mask,
+                             const int32_t* d_window_order, int32_t W, int32_t n,
+                             int32_t d, int32_t H, float scale, void* stream);
+
+/* Planned execution (no reference counterpart; the reference relies on the
+ * window sort alone, include/utils.cuh:48-59).  A plan splits windows with
+ * more than `seg_tiles` tiles (0 = automatic) into segments processed by
+ * separate waves and merged inside the same kernel launch, so hub windows do
+ * not serialise.  Build once per graph; reuse for every forward pass.
+ * A plan must not be used by two overlapping calls (it owns the merge
+ * counters). */
+typedef struct f3s_plan f3s_plan;
+f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_window_order,
+                           int32_t W, int32_t H, int32_t seg_tiles, void* stream,
+                           f3s_plan** plan_out);
+f3s_status f3s_plan_destroy(f3s_plan* plan);
+f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_split_windows,
+                         int64_t* T, int32_t* seg_tiles);
+f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q,
+                                     const uint16_t* K, const uint16_t* V, float* O,
+                                     const int32_t* d_block_col, const uint16_t* d_tile_mask,
+                                     int32_t n, int32_t d, int32_t H, float scale,
+                                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
