@@ -1,0 +1,202 @@
+"""Benchmark of the fused sparse graph-attention pass on one MI355X.
+
+Workload (config 4): 1,000,000-node power-law graph (mean degree 16,
+exponent 2.2, random node order, self-loops), d = 64, one head, Q/K/V
+~ N(0, 1) in fp16, edge-exact (masked) semantics, windows in descending
+workload order with heavy windows split by the plan.  A step is one fused
+pass over the whole graph with inputs already resident in HBM.
+
+Prints one JSON line: whole-job edges/s over K timed steps, the roofline
+of the fused kernel (algorithmic bytes / average launch time measured with
+HIP events on the launch stream) and the reference's own CPU baseline
+(baselines/cpu_baseline.cpp, compiled under oracle/_ref) timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA
+
+
+def alg_bytes(n: int, W: int, T: int, occ_sum: int, H: int, d: int, masked: bool) -> int:
+    """Algorithmic HBM bytes of one pass: Q fp16 and O fp32 per row, window
+    offsets + order, per tile a column index (+ 32 B of row masks when
+    masked) and one K and one V fp16 row per attended (tile, column)."""
+    return (n * H * d * (2 + 4) + (W + 1) * 4 + W * 4 + T * (4 + (32 if masked else 0))
+            + occ_sum * H * d * 2 * 2)
+
+
+def read_traffic(kernel_prefix: str) -> float | None:
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (profiles/pmc_traffic_cfg4.txt: 'bytes_per_launch <value>'), if any."""
+    p = ROOT / "profiles" / "pmc_traffic_cfg4.txt"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 2 and parts[0] == "bytes_per_launch":
+            return float(parts[1])
+    return None
+
+
+def cpu_baseline(rp, ci, Q, K, V, n: int, d: int) -> dict | None:
+    """The reference's cpu_sparse_attention_csr (single thread) over the
+    whole graph, on this host."""
+    ref = ROOT / "oracle" / "_ref" / "libref_cpu_baseline.so"
+    kind = "reference"
+    if not ref.exists():
+        return None
+    lib = C.CDLL(str(ref))
+    fn = lib.ref_cpu_sparse_attention_csr
+    fn.restype = None
+    fn.argtypes = [C.c_int32, C.c_int32] + [C.c_void_p] * 6
+    Qf, Kf, Vf = (np.ascontiguousarray(x.reshape(n, d), np.float32) for x in (Q, K, V))
+    O = np.zeros((n, d), np.float32)
+    t0 = time.perf_counter()
+    fn(n, d, Qf.ctypes.data, Kf.ctypes.data, Vf.ctypes.data, rp.ctypes.data, ci.ctypes.data,
+       O.ctypes.data)
+    dt = time.perf_counter() - t0
+    edges = int(rp[n])
+    return {"value": edges / dt, "unit": "edges/s", "cores": 1, "kind": kind,
+            "sample": f"all {n} rows / {edges} edges of the workload, one call, "
+                      f"{dt:.2f} s on {os.cpu_count()} visible host cores (1 used)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=4)
+    ap.add_argument("--semantics", choices=["masked", "tile_dense"], default="masked")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run device-to-device copies of this size (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters against known bytes) and exit")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the path shards "
+              "by row-window range with a K/V all-gather, which is not built here.",
+              file=sys.stderr)
+        return 2
+
+    import fused3s_amd as f3s
+
+    if f3s.device_count() < 1:
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    if args.copy_probe_mib:
+        nb = args.copy_probe_mib << 20
+        src = f3s.DeviceArray(nb, np.uint8, zero=True)
+        dst = f3s.DeviceArray(nb, np.uint8)
+        from fused3s_amd import _lib
+        for _ in range(args.steps):
+            _lib.hip().f3s_memcpy_d2d(dst.ptr, src.ptr, nb, None)
+        f3s.synchronize()
+        print(json.dumps({"copy_probe_bytes": nb, "launches": args.steps}), flush=True)
+        return 0
+    c = f3s.CONFIGS[args.config]
+    masked = args.semantics == "masked"
+    t0 = time.time()
+    rp, ci = c.graph()
+    n, H, d = c.n, c.H, c.d
+    nnz = int(len(ci))
+    Q, K, V = (c.features(t) for t in range(3))
+    print(f"[bench] cfg{c.cfg} {c.name}: n={n} nnz={nnz} H={H} inputs in {time.time()-t0:.1f}s",
+          file=sys.stderr, flush=True)
+
+    stream = f3s.Stream()
+    csr = f3s.DeviceCSR(rp, ci, stream)
+    ev0, ev1 = f3s.Event(), f3s.Event()
+    # converter (timed separately; not part of a step)
+    bsf = f3s.convert_device(csr, masks=True, stream=stream)
+    ev0.record(stream)
+    bsf = f3s.convert_device(csr, masks=True, stream=stream)
+    ev1.record(stream)
+    conv_ms = ev0.elapsed_ms(ev1)
+    order = f3s.window_order_device(bsf, stream)
+    plan = f3s.Plan(bsf, order, H=H, stream=stream)
+    occ_sum, mask_bits = f3s.bsf_stats(bsf, masked, stream)
+    dQ, dK, dV = (f3s.DeviceArray.from_numpy(x.view(np.uint16), stream) for x in (Q, K, V))
+    dO = f3s.DeviceArray((n, H, d), np.float32)
+    print(f"[bench] W={bsf.W} T={bsf.T} occ={occ_sum} items={plan.num_items} "
+          f"split={plan.num_split} seg={plan.seg_tiles} convert={conv_ms:.2f}ms",
+          file=sys.stderr, flush=True)
+
+    # cold first launch (the reference times exactly this, tests/test_fused_3s_v2.cu:126-137)
+    ev0.record(stream)
+    plan.forward(dQ, dK, dV, dO, masked=masked, stream=stream)
+    ev1.record(stream)
+    cold_ms = ev0.elapsed_ms(ev1)
+    for _ in range(args.warmup):
+        plan.forward(dQ, dK, dV, dO, masked=masked, stream=stream)
+    stream.synchronize()
+
+    # timed region: K steps bracketed by synchronisation; one event pair per
+    # launch on the launch stream gives the kernel's own duration
+    evs = [(f3s.Event(), f3s.Event()) for _ in range(args.steps)]
+    f3s.synchronize()
+    t_start = time.perf_counter()
+    for a, b in evs:
+        a.record(stream)
+        plan.forward(dQ, dK, dV, dO, masked=masked, stream=stream)
+        b.record(stream)
+    stream.synchronize()
+    f3s.synchronize()
+    wall = time.perf_counter() - t_start
+    kern_ms = np.array([a.elapsed_ms(b) for a, b in evs])
+    ms_per_step = wall * 1e3 / args.steps
+    kavg = float(kern_ms.mean())
+
+    nbytes = alg_bytes(n, bsf.W, bsf.T, occ_sum, H, d, masked)
+    achieved = nbytes / (kavg * 1e-3) / 1e9
+    flops_tile = bsf.T * 4 * 16 * 16 * d * H
+    traffic = read_traffic("fused_attention_kernel")
+    res = {
+        "metric": "fused attention edges/s + kernel us; achieved HBM GB/s (% of peak) on 1 MI355X",
+        "value": nnz * args.steps / wall,
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 in, f32 accumulate/softmax/out",
+        "data": "synthetic (seeded generator; no dataset download)",
+        "config": {"workload": f"cfg{c.cfg}: {c.name}", "nodes": n, "edges": nnz, "heads": H,
+                   "head_dim": d, "semantics": args.semantics, "row_windows": bsf.W,
+                   "active_tiles": bsf.T, "attended_tile_columns": occ_sum},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
+        "cpu_baseline": None,
+        "kernel_us": {"mean": kavg * 1e3, "min": float(kern_ms.min()) * 1e3,
+                      "median": float(np.median(kern_ms)) * 1e3, "cold_first_launch": cold_ms * 1e3},
+        "alg_bytes_per_launch": nbytes,
+        "mfma_frac_tile_model": flops_tile / (kavg * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
+        "converter_us": conv_ms * 1e3,
+        "device": f3s.device_name(),
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] timing the reference CPU baseline ...", file=sys.stderr, flush=True)
+        res["cpu_baseline"] = cpu_baseline(rp, ci, Q.astype(np.float32), K.astype(np.float32),
+                                           V.astype(np.float32), n, d) if H == 1 else None
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
