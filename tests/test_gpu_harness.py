@@ -1,0 +1,32 @@
+"""The C++ launch/verify harness (drop-in counterpart of the reference's
+tests/test_fused_3s_v2.cu) and the driver's smoke entry, run on the GPU."""
+from __future__ import annotations
+
+import subprocess
+
+import pytest
+
+from conftest import GOLDEN, ROOT
+
+pytestmark = pytest.mark.gpu
+EXE = ROOT / "tests" / "cpp" / "bin" / "test_fused_3s"
+
+
+@pytest.mark.parametrize("args", [
+    [str(GOLDEN / "cora")],
+    [str(GOLDEN / "cora"), "--semantics", "tile_dense"],
+    [str(GOLDEN / "citeseer")],
+    ["--config", "3", "--semantics", "tile_dense"],
+])
+def test_harness(gpu, args):
+    assert EXE.exists(), "harness binary missing: run __graft_entry__.build()"
+    r = subprocess.run([str(EXE), *args, "--reps", "5"], capture_output=True, text=True,
+                       timeout=120)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stderr
+    assert "SUCCESS" in r.stdout and "bit-exact" in r.stdout
+
+
+def test_smoke_entry(gpu):
+    import __graft_entry__ as ge
+    ge.smoke()
