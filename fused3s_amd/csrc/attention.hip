@@ -15,10 +15,10 @@
 // Work decomposition (one wave = one (item, head)):
 //   An item is a row window or, in a plan, a segment of a heavy window.
 //   The wave expands its tiles into a list of attended columns ("slots"),
-//   each with a 16-bit row mask, held in a per-wave LDS ring: 64 tiles per
-//   step, one tile per lane, positions from a wave prefix sum.  Columns no
-//   row attends are never gathered (column compaction).  Slots are consumed
-//   32 at a time:
+//   each with the mask of the window rows that attend it, held in a per-wave
+//   LDS ring: 64 tiles per step, one tile per lane, positions from a DPP
+//   wave prefix sum.  Columns no row attends are never gathered (column
+//   compaction).  Slots are consumed 32 at a time:
 //     S^T[32 x 16] = K_slots[32 x 64] . Q_w^T    4 MFMA 16x16x32 (K gathered
 //                                                straight into A operands)
 //     masked online softmax, row r in lanes r, r+16, r+32, r+48
@@ -29,6 +29,8 @@
 //   (scale_fragment_by_row, src/fused3s_v2.cu:54-71) is a plain multiply by
 //   the lane's own correction: no shuffles, no LDS round trip for P.
 //   Q stays in registers in B-operand layout for the whole item.
+//   Segments of split windows write (m, l, O) partials; merge_partials_kernel
+//   combines them in slot order in a second, small launch.
 //
 // MFMA 16x16x32 f16 operand layout used (CDNA3/CDNA4 16x16 family): lane l
 // supplies row l%16 of A and column l%16 of B, 8 consecutive k per lane in
@@ -38,8 +40,6 @@
 // code relies only on that and on the row/column/C mapping.
 #include <math.h>
 #include <stdio.h>
-
-#include <vector>
 
 #include "f3s_common.hpp"
 #include "f3s_device.hpp"
@@ -51,11 +51,16 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 64;             // feature dim per head (FEAT_DIM_FIXED, fused3s_v2.cu:41)
+constexpr int kRowBytes = kD * 2;  // one fp16 K/V/Q row of one head
 constexpr int kChunk = 32;         // attended columns per MFMA step
 constexpr int kRing = 256;         // column ring entries per wave
-constexpr int kWavesPerWG = 4;
-constexpr int kThreads = kWave * kWavesPerWG;
 constexpr int kPartialFloats = 16 * kD + 32;   // O[16][64], m[16], l[16]
+constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
+// Word 3 of a raw buffer descriptor for the gfx9 family (incl. gfx950):
+// 32-bit data format, no swizzle.  Offsets >= num_records read as 0.
+constexpr int32_t kBufferFlags = 0x00020000;
+// Row-mask layout in the ring: bit k = row 2k, bit 16 + k = row 2k + 1.
+constexpr uint32_t kAllRows = 0x00ff00ffu;
 
 struct Item {
     int32_t w, tb, te, slot;       // slot < 0: whole window, write O directly
@@ -67,9 +72,42 @@ struct SplitInfo {
 
 struct __align__(16) WaveLds {
     int32_t col[kRing];
-    uint16_t rm[kRing];
+    uint32_t rm[kRing];
     _Float16 v[kChunk * kD];
 };
+
+struct AttnParams {
+    const _Float16* Q;
+    const _Float16* K;
+    const _Float16* V;
+    float* O;
+    const int32_t* window_offsets;   // unplanned launch only
+    const int32_t* block_col;
+    const uint16_t* tile_mask;       // NULL: tile-dense semantics
+    const int32_t* window_order;     // unplanned launch only (NULL: natural order)
+    const Item* items;               // planned launch (NULL: one item per window)
+    int64_t num_items;
+    int32_t W, n;
+    float scale_log2;
+    int32_t xcd_contiguous;          // map consecutive items to the same XCD
+    uint32_t feat_bytes;             // bytes of Q (= K = V), < 2^32
+    float* partials;
+    const SplitInfo* splits;
+    int64_t num_split;
+};
+
+// Workgroup index -> logical block.  The dispatcher deals workgroups to the
+// 8 XCDs round-robin; with `xcd_contiguous` each XCD instead receives one
+// contiguous range of logical blocks, so windows that share neighbours
+// (community-ordered graphs) share one XCD's L2.
+__device__ __forceinline__ int64_t logical_block(int32_t xcd_contiguous)
+{
+    const int64_t b = blockIdx.x;
+    if (!xcd_contiguous) return b;
+    const int64_t G = gridDim.x;
+    const int64_t x = b % kXcds, q = G / kXcds, rem = G % kXcds;
+    return x * q + min(x, rem) + b / kXcds;
+}
 
 __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c)
 {
@@ -78,63 +116,97 @@ __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c)
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             kBufferFlags);
+}
+
+__device__ __forceinline__ h8 load_h8(__amdgpu_buffer_rsrc_t rs, uint32_t off)
+{
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    return __builtin_bit_cast(h8, v);
+}
+
+// Inclusive prefix sum over the wave with DPP row shifts and row broadcasts.
+__device__ __forceinline__ int wave_scan_incl(int x)
+{
+    int s = x;
+    s += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+    s += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+    s += __builtin_amdgcn_update_dpp(0, x, 0x113, 0xf, 0xf, true);   // row_shr:3
+    s += __builtin_amdgcn_update_dpp(0, s, 0x114, 0xf, 0xe, true);   // row_shr:4, lanes 4-15
+    s += __builtin_amdgcn_update_dpp(0, s, 0x118, 0xf, 0xc, true);   // row_shr:8, lanes 8-15
+    s += __builtin_amdgcn_update_dpp(0, s, 0x142, 0xa, 0xf, true);   // row_bcast:15 -> rows 1, 3
+    s += __builtin_amdgcn_update_dpp(0, s, 0x143, 0xc, 0xf, true);   // row_bcast:31 -> rows 2, 3
+    return s;
+}
+
+// Rows of a tile that attend its column c, from the tile's 16 row masks
+// packed two per word (word k = rows 2k | 2k+1 << 16).
+__device__ __forceinline__ uint32_t column_rows(const uint32_t (&wd)[8], int c)
+{
+    uint32_t x = (wd[0] >> c) & 0x00010001u;
+#pragma unroll
+    for (int k = 1; k < 8; ++k) x |= ((wd[k] >> c) & 0x00010001u) << k;
+    return x;
+}
+
 // Slot order of the 8 logits a lane holds (lane group g): S^T tile 0 rows
 // 4g..4g+3, then tile 1 rows 16+4g..16+4g+3.  Used as the k order of P.V.
 __device__ __forceinline__ int slot_of(int g, int j) { return (j < 4) ? 4 * g + j : 16 + 4 * g + (j - 4); }
 
-template <int H, bool MASKED>
-__global__ void __launch_bounds__(kThreads)
-fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
-                       const _Float16* __restrict__ V, float* __restrict__ O,
-                       const int32_t* __restrict__ window_offsets,
-                       const int32_t* __restrict__ block_col,
-                       const uint16_t* __restrict__ tile_mask,
-                       const int32_t* __restrict__ window_order,
-                       const Item* __restrict__ items, int64_t num_items, int32_t W, int32_t n,
-                       float scale_log2, float* __restrict__ partials,
-                       int32_t* __restrict__ counters, const SplitInfo* __restrict__ splits,
-                       const int32_t* __restrict__ slot_split)
+// WPG waves per workgroup; each wave processes one (item, head).  The
+// register budget is capped for 4 waves per SIMD.
+template <int H, bool MASKED, int WPG>
+__global__ void __launch_bounds__(kWave * WPG) __attribute__((amdgpu_waves_per_eu(4)))
+fused_attention_kernel(const AttnParams p)
 {
-    __shared__ WaveLds lds_all[kWavesPerWG];
+    __shared__ WaveLds lds_all[WPG];
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    const int g = lane >> 4;     // lane group
-    const int r = lane & 15;     // row of the window this lane owns (and MFMA column)
+    const int g = lane >> 4;                          // lane group
+    const int r = lane & 15;                          // row of the window this lane owns
+    const int rbit = (r & 1) ? 16 + (r >> 1) : (r >> 1);   // row r in a ring row mask
     WaveLds& L = lds_all[wave];
 
-    const int64_t gw = (int64_t)blockIdx.x * kWavesPerWG + wave;
+    const int32_t n = p.n;
+    const int64_t gw = logical_block(p.xcd_contiguous) * WPG + wave;
     const int64_t item_idx = gw / H;
     const int h = (int)(gw % H);
-    if (item_idx >= num_items) return;
+    if (item_idx >= p.num_items) return;
 
     // ---- item decode (wave-uniform) ----
     int32_t w, tb, te, slot;
-    if (items) {
-        const Item it = items[item_idx];
+    if (p.items) {
+        const Item it = p.items[item_idx];
         w = it.w;
         tb = it.tb;
         te = it.te;
         slot = it.slot;
     } else {
-        w = window_order ? window_order[item_idx] : (int32_t)item_idx;
-        if (w < 0 || w >= W) return;
-        tb = window_offsets[w];
-        te = window_offsets[w + 1];
+        w = p.window_order ? p.window_order[item_idx] : (int32_t)item_idx;
+        if (w < 0 || w >= p.W) return;
+        const int32_t T = p.window_offsets[p.W];
+        tb = max(0, min(p.window_offsets[w], T));
+        te = max(tb, min(p.window_offsets[w + 1], T));
         slot = -1;
-        const int32_t T = window_offsets[W];
-        tb = max(0, min(tb, T));
-        te = max(tb, min(te, T));
     }
     const int32_t nbc = (n + 15) >> 4;   // valid block columns
+    const int32_t* __restrict__ block_col = p.block_col;
+    const uint16_t* __restrict__ tile_mask = p.tile_mask;
+    const __amdgpu_buffer_rsrc_t qres = make_rsrc(p.Q, p.feat_bytes);
+    const __amdgpu_buffer_rsrc_t kres = make_rsrc(p.K, p.feat_bytes);
+    const __amdgpu_buffer_rsrc_t vres = make_rsrc(p.V, p.feat_bytes);
+    const uint32_t head_off = (uint32_t)h * kRowBytes;
+    constexpr uint32_t kNoRow = 0xfffffff0u;   // out of range (and no 32-bit wrap): loads return 0
 
     // ---- Q tile in registers, B-operand layout ----
     const int32_t qrow = w * 16 + r;
-    h8 q0 = {}, q1 = {};
-    if (qrow < n) {
-        const _Float16* qp = Q + ((int64_t)qrow * H + h) * kD;
-        q0 = *reinterpret_cast<const h8*>(qp + 8 * g);
-        q1 = *reinterpret_cast<const h8*>(qp + 32 + 8 * g);
-    }
+    const uint32_t qoff = qrow < n ? (uint32_t)qrow * (H * kRowBytes) + head_off + 16 * g : kNoRow;
+    const h8 q0 = load_h8(qres, qoff);
+    const h8 q1 = load_h8(qres, qoff == kNoRow ? kNoRow : qoff + 64);
 
     float m = -INFINITY;   // running max of row r (log2 domain)
     float l = 0.f;         // this lane's share of the running sum of row r
@@ -142,7 +214,7 @@ fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restric
                  {0.f, 0.f, 0.f, 0.f}};
 
     int32_t tcur = tb;
-    int32_t head = 0, tail = 0;   // ring positions (monotone)
+    int32_t head = 0, tail = 0;   // ring positions (monotone, wave-uniform)
     constexpr int32_t kMask = kRing - 1;
 
     while (true) {
@@ -151,17 +223,18 @@ fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restric
             const int32_t t = tcur + lane;
             uint32_t u = 0;
             int32_t bc = 0;
-            uint4 mlo = make_uint4(0, 0, 0, 0), mhi = make_uint4(0, 0, 0, 0);
+            uint32_t wd[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             if (t < te) {
                 bc = block_col[t];
-                if (bc >= 0 && bc < nbc) {
+                if ((uint32_t)bc < (uint32_t)nbc) {
                     const int32_t left = n - bc * 16;
                     const uint32_t valid = left >= 16 ? 0xffffu : ((1u << left) - 1u);
                     if (MASKED) {
                         const uint4* mp = reinterpret_cast<const uint4*>(tile_mask + (int64_t)t * 16);
-                        mlo = mp[0];
-                        mhi = mp[1];
-                        uint32_t o = mlo.x | mlo.y | mlo.z | mlo.w | mhi.x | mhi.y | mhi.z | mhi.w;
+                        const uint4 a = mp[0], b = mp[1];
+                        wd[0] = a.x; wd[1] = a.y; wd[2] = a.z; wd[3] = a.w;
+                        wd[4] = b.x; wd[5] = b.y; wd[6] = b.z; wd[7] = b.w;
+                        const uint32_t o = a.x | a.y | a.z | a.w | b.x | b.y | b.z | b.w;
                         u = (o | (o >> 16)) & valid;
                     } else {
                         u = valid;
@@ -169,30 +242,19 @@ fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restric
                 }
             }
             const int occ = __popc(u);
-            const int incl = wave_inclusive_scan(occ);
+            const int incl = wave_scan_incl(occ);
             const int avail = kRing - (tail - head);
             const bool accept = (t < te) && incl <= avail;
-            const uint64_t bal = __ballot(accept);
-            const int nacc = __popcll(bal);
-            const int added = __shfl(incl, nacc - 1, kWave);
+            const int nacc = __popcll(__ballot(accept));          // accepted lanes: a prefix
+            const int added = __builtin_amdgcn_readlane(incl, nacc - 1);
             if (accept && occ) {
                 int32_t pos = tail + incl - occ;
-                const uint32_t words[8] = {mlo.x, mlo.y, mlo.z, mlo.w, mhi.x, mhi.y, mhi.z, mhi.w};
                 uint32_t rest = u;
                 while (rest) {
                     const int c = __ffs(rest) - 1;
                     rest &= rest - 1;
-                    uint32_t rmask = 0xffffu;
-                    if (MASKED) {
-                        rmask = 0;
-#pragma unroll
-                        for (int k = 0; k < 8; ++k) {
-                            rmask |= ((words[k] >> c) & 1u) << (2 * k);
-                            rmask |= ((words[k] >> (16 + c)) & 1u) << (2 * k + 1);
-                        }
-                    }
                     L.col[pos & kMask] = bc * 16 + c;
-                    L.rm[pos & kMask] = (uint16_t)rmask;
+                    L.rm[pos & kMask] = MASKED ? column_rows(wd, c) : kAllRows;
                     ++pos;
                 }
             }
@@ -205,27 +267,26 @@ fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restric
         F3S_WAVE_LDS_SYNC();
 
         // ---- gather K (A operands) and V (for LDS) of this chunk ----
-        const int32_t pad_col = L.col[head & kMask];
-        const int32_t c0 = (r < cnt) ? L.col[(head + r) & kMask] : pad_col;
-        const int32_t c1 = (16 + r < cnt) ? L.col[(head + 16 + r) & kMask] : pad_col;
-        const _Float16* k0p = K + ((int64_t)c0 * H + h) * kD;
-        const _Float16* k1p = K + ((int64_t)c1 * H + h) * kD;
-        const h8 ka0 = *reinterpret_cast<const h8*>(k0p + 8 * g);
-        const h8 ka1 = *reinterpret_cast<const h8*>(k0p + 32 + 8 * g);
-        const h8 kb0 = *reinterpret_cast<const h8*>(k1p + 8 * g);
-        const h8 kb1 = *reinterpret_cast<const h8*>(k1p + 32 + 8 * g);
+        auto row_off = [&](int s) -> uint32_t {
+            return s < cnt ? (uint32_t)L.col[(head + s) & kMask] * (H * kRowBytes) + head_off
+                           : kNoRow;
+        };
+        const uint32_t k0 = row_off(r), k1 = row_off(16 + r);
+        const h8 ka0 = load_h8(kres, k0 == kNoRow ? kNoRow : k0 + 16 * g);
+        const h8 ka1 = load_h8(kres, k0 == kNoRow ? kNoRow : k0 + 64 + 16 * g);
+        const h8 kb0 = load_h8(kres, k1 == kNoRow ? kNoRow : k1 + 16 * g);
+        const h8 kb1 = load_h8(kres, k1 == kNoRow ? kNoRow : k1 + 64 + 16 * g);
         h8 vrow[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int s = (lane >> 3) + 8 * i;
-            const int32_t cv = (s < cnt) ? L.col[(head + s) & kMask] : pad_col;
-            vrow[i] = *reinterpret_cast<const h8*>(V + ((int64_t)cv * H + h) * kD + 8 * (lane & 7));
+            const uint32_t vo = row_off((lane >> 3) + 8 * i);
+            vrow[i] = load_h8(vres, vo == kNoRow ? kNoRow : vo + 16 * (lane & 7));
         }
         uint32_t rmv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int s = slot_of(g, j);
-            rmv[j] = (s < cnt) ? (uint32_t)L.rm[(head + s) & kMask] : 0u;
+            rmv[j] = s < cnt ? L.rm[(head + s) & kMask] : 0u;
         }
 
         // ---- S^T = K . Q^T ----
@@ -239,8 +300,8 @@ fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restric
         float x[8];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            x[v] = ((rmv[v] >> r) & 1u) ? s0[v] * scale_log2 : -INFINITY;
-            x[4 + v] = ((rmv[4 + v] >> r) & 1u) ? s1[v] * scale_log2 : -INFINITY;
+            x[v] = ((rmv[v] >> rbit) & 1u) ? s0[v] * p.scale_log2 : -INFINITY;
+            x[4 + v] = ((rmv[4 + v] >> rbit) & 1u) ? s1[v] * p.scale_log2 : -INFINITY;
         }
         float cm = x[0];
 #pragma unroll
@@ -254,9 +315,9 @@ fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restric
         float ls = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const _Float16 p = (_Float16)fast_exp2(x[j] - mu);
-            pb[j] = p;
-            ls += (float)p;   // the sum uses the rounded weights P.V uses
+            const _Float16 pj = (_Float16)fast_exp2(x[j] - mu);
+            pb[j] = pj;
+            ls += (float)pj;   // the sum uses the rounded weights P.V uses
         }
         l = l * corr + ls;
         m = mn;
@@ -293,7 +354,7 @@ fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restric
     if (slot < 0) {
         const float inv = lrow > 0.f ? 1.0f / lrow : 0.f;
         if (orow < n) {
-            float* op = O + ((int64_t)orow * H + h) * kD + 16 * g;
+            float* op = p.O + ((int64_t)orow * H + h) * kD + 16 * g;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 float4 o4 = make_float4(acc[0][v] * inv, acc[1][v] * inv, acc[2][v] * inv,
@@ -303,48 +364,49 @@ fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restric
         }
         return;
     }
-
-    // Segment of a split window: publish (m, l, O) and let the last segment
-    // of this (window, head) merge all of them in slot order.
-    float* part = partials + ((int64_t)slot * H + h) * kPartialFloats;
-    {
-        float* op = part + r * kD + 16 * g;
+    // Segment of a split window: publish (m, l, unnormalised O) for the merge.
+    float* part = p.partials + ((int64_t)slot * H + h) * kPartialFloats;
+    float* op = part + r * kD + 16 * g;
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-            *reinterpret_cast<float4*>(op + 4 * v) =
-                make_float4(acc[0][v], acc[1][v], acc[2][v], acc[3][v]);
-        if (g == 0) {
-            part[16 * kD + r] = m;
-            part[16 * kD + 16 + r] = lrow;
-        }
+    for (int v = 0; v < 4; ++v)
+        *reinterpret_cast<float4*>(op + 4 * v) =
+            make_float4(acc[0][v], acc[1][v], acc[2][v], acc[3][v]);
+    if (g == 0) {
+        part[16 * kD + r] = m;
+        part[16 * kD + 16 + r] = lrow;
     }
-    __threadfence();
-    const int32_t sid = slot_split[slot];
-    const SplitInfo si = splits[sid];
-    int32_t old = 0;
-    if (lane == 0) old = atomicAdd(&counters[(int64_t)sid * H + h], 1);
-    old = __shfl(old, 0, kWave);
-    if (old != si.nseg - 1) return;
-    __threadfence();
+}
 
+// Combines the segments of each split window, in slot order (deterministic):
+// M = max m_k, O = sum O_k 2^(m_k - M) / sum l_k 2^(m_k - M).  One wave per
+// (split window, head); lane (g, r) owns row r, dims 16g..16g+15.
+template <int H>
+__global__ void __launch_bounds__(256) merge_partials_kernel(const AttnParams p)
+{
+    const int64_t gw = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int g = lane >> 4, r = lane & 15;
+    const int64_t sid = gw / H;
+    const int h = (int)(gw % H);
+    if (sid >= p.num_split) return;
+    const SplitInfo si = p.splits[sid];
+    auto part = [&](int k) {
+        return p.partials + ((int64_t)(si.first_slot + k) * H + h) * kPartialFloats;
+    };
     float M = -INFINITY;
-    for (int k = 0; k < si.nseg; ++k) {
-        const float* pk = partials + ((int64_t)(si.first_slot + k) * H + h) * kPartialFloats;
-        M = __builtin_fmaxf(M, pk[16 * kD + r]);
-    }
+    for (int k = 0; k < si.nseg; ++k) M = __builtin_fmaxf(M, part(k)[16 * kD + r]);
     float Ls = 0.f;
     float4 o[4] = {make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0),
                    make_float4(0, 0, 0, 0)};
     if (M != -INFINITY) {
         for (int k = 0; k < si.nseg; ++k) {
-            const float* pk = partials + ((int64_t)(si.first_slot + k) * H + h) * kPartialFloats;
-            const float mk = pk[16 * kD + r];
-            const float f = fast_exp2(mk - M);
+            const float* pk = part(k);
+            const float f = fast_exp2(pk[16 * kD + r] - M);
             Ls += pk[16 * kD + 16 + r] * f;
-            const float* op = pk + r * kD + 16 * g;
+            const float* src = pk + r * kD + 16 * g;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                float4 a = *reinterpret_cast<const float4*>(op + 4 * v);
+                const float4 a = *reinterpret_cast<const float4*>(src + 4 * v);
                 o[v].x += a.x * f;
                 o[v].y += a.y * f;
                 o[v].z += a.z * f;
@@ -353,15 +415,14 @@ fused_attention_kernel(const _Float16* __restrict__ Q, const _Float16* __restric
         }
     }
     const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
-    const int32_t mrow = si.w * 16 + r;
-    if (mrow < n) {
-        float* op = O + ((int64_t)mrow * H + h) * kD + 16 * g;
+    const int32_t row = si.w * 16 + r;
+    if (row < p.n) {
+        float* dst = p.O + ((int64_t)row * H + h) * kD + 16 * g;
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-            *reinterpret_cast<float4*>(op + 4 * v) =
+            *reinterpret_cast<float4*>(dst + 4 * v) =
                 make_float4(o[v].x * inv, o[v].y * inv, o[v].z * inv, o[v].w * inv);
     }
-    if (lane == 0) counters[(int64_t)sid * H + h] = 0;   // ready for the next launch
 }
 
 // ----------------------------------------------------------------- planner
@@ -389,7 +450,7 @@ __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __res
                           int32_t W, int32_t seg, const int64_t* __restrict__ item_base,
                           const int64_t* __restrict__ slot_base,
                           const int64_t* __restrict__ split_base, Item* __restrict__ items,
-                          SplitInfo* __restrict__ splits, int32_t* __restrict__ slot_split)
+                          SplitInfo* __restrict__ splits)
 {
     const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
     if (L >= W) return;
@@ -407,13 +468,10 @@ __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __res
         return;
     }
     const int32_t sb = (int32_t)slot_base[L];
-    const int32_t sid = (int32_t)split_base[L];
-    splits[sid] = SplitInfo{w, sb, ns, 0};
+    splits[split_base[L]] = SplitInfo{w, sb, ns, 0};
     for (int32_t k = 0; k < ns; ++k) {
         const int32_t a = tb + k * seg;
-        const int32_t b = min(te, a + seg);
-        items[ib + k] = Item{w, a, b, sb + k};
-        slot_split[sb + k] = sid;
+        items[ib + k] = Item{w, a, min(te, a + seg), sb + k};
     }
 }
 
@@ -421,8 +479,9 @@ __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __res
 
 struct f3s_plan {
     int32_t W = 0, H = 1, seg = 0;
+    int32_t natural_order = 1;   // no window order given: keep neighbours on one XCD
     int64_t T = 0, num_items = 0, num_split = 0, num_slots = 0;
-    f3s::DeviceBuffer items, splits, slot_split, partials, counters;
+    f3s::DeviceBuffer items, splits, partials;
 };
 
 namespace f3s {
@@ -442,51 +501,51 @@ static f3s_status check_attention_args(const void* Q, const void* K, const void*
     F3S_REQUIRE(n == 0 || (Q && K && V && O), "attention: NULL feature pointer");
     F3S_REQUIRE(((((uintptr_t)Q) | ((uintptr_t)K) | ((uintptr_t)V) | ((uintptr_t)O)) & 15) == 0,
                 "attention: Q, K, V, O must be 16-byte aligned");
+    if ((int64_t)n * H * kRowBytes >= ((int64_t)1 << 32) - 64) {
+        set_error("attention: Q/K/V larger than 4 GiB are not supported (32-bit buffer offsets)");
+        return F3S_EUNSUPPORTED;
+    }
     return F3S_OK;
 }
 
-template <int H>
-static void launch_h(bool masked, dim3 grid, hipStream_t st, const _Float16* Q, const _Float16* K,
-                     const _Float16* V, float* O, const int32_t* offs, const int32_t* bcol,
-                     const uint16_t* mask, const int32_t* order, const Item* items,
-                     int64_t num_items, int32_t W, int32_t n, float sl2, float* partials,
-                     int32_t* counters, const SplitInfo* splits, const int32_t* slot_split)
+template <int H, bool MASKED>
+static void launch_hm(const AttnParams& p, int64_t waves, hipStream_t st)
 {
-    if (masked)
-        hipLaunchKernelGGL((fused_attention_kernel<H, true>), grid, dim3(kThreads), 0, st, Q, K,
-                           V, O, offs, bcol, mask, order, items, num_items, W, n, sl2, partials,
-                           counters, splits, slot_split);
-    else
-        hipLaunchKernelGGL((fused_attention_kernel<H, false>), grid, dim3(kThreads), 0, st, Q, K,
-                           V, O, offs, bcol, mask, order, items, num_items, W, n, sl2, partials,
-                           counters, splits, slot_split);
+    // Small launches use one-wave workgroups so they spread over all CUs.
+    if (waves < 4 * 256 * 2) {
+        hipLaunchKernelGGL((fused_attention_kernel<H, MASKED, 1>), dim3((unsigned)waves),
+                           dim3(kWave), 0, st, p);
+    } else {
+        hipLaunchKernelGGL((fused_attention_kernel<H, MASKED, 4>),
+                           dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
+    }
+    if (p.num_split > 0)
+        hipLaunchKernelGGL(merge_partials_kernel<H>, dim3((unsigned)ceil_div(p.num_split * H, 4)),
+                           dim3(256), 0, st, p);
 }
 
-static f3s_status launch(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,
-                         const int32_t* offs, const int32_t* bcol, const uint16_t* mask,
-                         const int32_t* order, const Item* items, int64_t num_items, int32_t W,
-                         int32_t n, int32_t H, float scale, float* partials, int32_t* counters,
-                         const SplitInfo* splits, const int32_t* slot_split, hipStream_t st)
+template <int H>
+static void launch_h(const AttnParams& p, int64_t waves, hipStream_t st)
 {
-    if (num_items <= 0) return F3S_OK;
-    const int64_t waves = num_items * H;
-    const int64_t blocks = ceil_div(waves, kWavesPerWG);
-    F3S_REQUIRE(blocks < ((int64_t)1 << 31), "attention: too many work items");
-    const float sl2 = scale * 1.4426950408889634f;
-    const dim3 grid((unsigned)blocks);
-    auto q = reinterpret_cast<const _Float16*>(Q);
-    auto k = reinterpret_cast<const _Float16*>(K);
-    auto v = reinterpret_cast<const _Float16*>(V);
-    const bool masked = mask != nullptr;
-    if (H == 1)
-        launch_h<1>(masked, grid, st, q, k, v, O, offs, bcol, mask, order, items, num_items, W,
-                    n, sl2, partials, counters, splits, slot_split);
-    else if (H == 2)
-        launch_h<2>(masked, grid, st, q, k, v, O, offs, bcol, mask, order, items, num_items, W,
-                    n, sl2, partials, counters, splits, slot_split);
+    if (p.tile_mask)
+        launch_hm<H, true>(p, waves, st);
     else
-        launch_h<4>(masked, grid, st, q, k, v, O, offs, bcol, mask, order, items, num_items, W,
-                    n, sl2, partials, counters, splits, slot_split);
+        launch_hm<H, false>(p, waves, st);
+}
+
+static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
+{
+    if (p.num_items <= 0) return F3S_OK;
+    const int64_t waves = p.num_items * H;
+    F3S_REQUIRE(waves < ((int64_t)1 << 31), "attention: too many work items");
+    p.scale_log2 = scale * 1.4426950408889634f;
+    p.feat_bytes = (uint32_t)((int64_t)p.n * H * kRowBytes);
+    if (H == 1)
+        launch_h<1>(p, waves, st);
+    else if (H == 2)
+        launch_h<2>(p, waves, st);
+    else
+        launch_h<4>(p, waves, st);
     F3S_HIP(hipGetLastError());
     return F3S_OK;
 }
@@ -510,8 +569,20 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
     F3S_REQUIRE((((uintptr_t)d_tile_mask) & 15) == 0, "f3s_attention_fwd: tile_mask alignment");
     F3S_TRY(require_device());
     clear_error();
-    return launch(Q, K, V, O, d_window_offsets, d_block_col, d_tile_mask, d_window_order, nullptr,
-                  W, W, n, H, scale, nullptr, nullptr, nullptr, nullptr, as_stream(stream));
+    AttnParams p{};
+    p.Q = reinterpret_cast<const _Float16*>(Q);
+    p.K = reinterpret_cast<const _Float16*>(K);
+    p.V = reinterpret_cast<const _Float16*>(V);
+    p.O = O;
+    p.window_offsets = d_window_offsets;
+    p.block_col = d_block_col;
+    p.tile_mask = d_tile_mask;
+    p.window_order = d_window_order;
+    p.num_items = W;
+    p.W = W;
+    p.n = n;
+    p.xcd_contiguous = d_window_order == nullptr;
+    return launch(p, H, scale, as_stream(stream));
 }
 
 f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_window_order,
@@ -531,6 +602,7 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     f3s_plan* p = new f3s_plan();
     p->W = W;
     p->H = H;
+    p->natural_order = d_window_order == nullptr;
     int32_t T32 = 0;
     if (W > 0) {
         F3S_HIP(hipMemcpyAsync(&T32, d_window_offsets + W, sizeof T32, hipMemcpyDeviceToHost, st));
@@ -542,7 +614,7 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     int64_t seg = seg_tiles;
     if (seg == 0) {
         seg = ceil_div(p->T * H, 8192);
-        if (seg < 64) seg = 64;
+        if (seg < 16) seg = 16;
     }
     if (seg > INT32_MAX) seg = INT32_MAX;
     p->seg = (int32_t)seg;
@@ -588,20 +660,14 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     p->num_split = totals[2];
     if ((s = p->items.reserve(sizeof(Item) * (size_t)(p->num_items + 1))) != F3S_OK ||
         (s = p->splits.reserve(sizeof(SplitInfo) * (size_t)(p->num_split + 1))) != F3S_OK ||
-        (s = p->slot_split.reserve(sizeof(int32_t) * (size_t)(p->num_slots + 1))) != F3S_OK ||
         (s = p->partials.reserve(sizeof(float) * (size_t)kPartialFloats * H *
-                                 (size_t)(p->num_slots + 1))) != F3S_OK ||
-        (s = p->counters.reserve(sizeof(int32_t) * (size_t)H * (size_t)(p->num_split + 1))) !=
-            F3S_OK)
+                                 (size_t)(p->num_slots + 1))) != F3S_OK)
         return fail(s);
-    if (hipMemsetAsync(p->counters.ptr, 0, p->counters.bytes, st) != hipSuccess)
-        return fail(hip_fail(hipGetLastError(), "plan counters", __FILE__, __LINE__));
     if (W > 0) {
         hipLaunchKernelGGL(plan_fill, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
                            d_window_offsets, d_window_order, W, p->seg, bi, bs, bp,
                            reinterpret_cast<Item*>(p->items.ptr),
-                           reinterpret_cast<SplitInfo*>(p->splits.ptr),
-                           reinterpret_cast<int32_t*>(p->slot_split.ptr));
+                           reinterpret_cast<SplitInfo*>(p->splits.ptr));
         if (hipGetLastError() != hipSuccess) return fail(F3S_EHIP);
     }
     if (hipStreamSynchronize(st) != hipSuccess)
@@ -642,12 +708,22 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
                 "f3s_attention_fwd_planned: tile_mask alignment");
     F3S_TRY(require_device());
     clear_error();
-    return launch(Q, K, V, O, nullptr, d_block_col, d_tile_mask, nullptr,
-                  reinterpret_cast<const Item*>(plan->items.ptr), plan->num_items, plan->W, n, H,
-                  scale, reinterpret_cast<float*>(plan->partials.ptr),
-                  reinterpret_cast<int32_t*>(plan->counters.ptr),
-                  reinterpret_cast<const SplitInfo*>(plan->splits.ptr),
-                  reinterpret_cast<const int32_t*>(plan->slot_split.ptr), as_stream(stream));
+    AttnParams p{};
+    p.Q = reinterpret_cast<const _Float16*>(Q);
+    p.K = reinterpret_cast<const _Float16*>(K);
+    p.V = reinterpret_cast<const _Float16*>(V);
+    p.O = O;
+    p.block_col = d_block_col;
+    p.tile_mask = d_tile_mask;
+    p.items = reinterpret_cast<const Item*>(plan->items.ptr);
+    p.num_items = plan->num_items;
+    p.W = plan->W;
+    p.n = n;
+    p.xcd_contiguous = plan->natural_order;
+    p.partials = reinterpret_cast<float*>(plan->partials.ptr);
+    p.splits = reinterpret_cast<const SplitInfo*>(plan->splits.ptr);
+    p.num_split = plan->num_split;
+    return launch(p, H, scale, as_stream(stream));
 }
 
 }  // extern "C"
