@@ -84,6 +84,8 @@ def main() -> int:
     ap.add_argument("--order", choices=["auto", "sorted", "natural"], default="auto",
                     help="window order: descending workload (the reference's sort) or natural; "
                          "auto = natural for the community-ordered SBM config, else sorted")
+    ap.add_argument("--seg", type=int, default=0,
+                    help="plan segment size in tiles (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run device-to-device copies of this size (calibrates the "
@@ -110,6 +112,7 @@ def main() -> int:
         f3s.synchronize()
         print(json.dumps({"copy_probe_bytes": nb, "launches": args.steps}), flush=True)
         return 0
+    f3s.init()
     c = f3s.CONFIGS[args.config]
     masked = args.semantics == "masked"
     t0 = time.time()
@@ -131,7 +134,7 @@ def main() -> int:
     conv_ms = ev0.elapsed_ms(ev1)
     use_sorted = args.order == "sorted" or (args.order == "auto" and c.kind != "sbm")
     order = f3s.window_order_device(bsf, stream) if use_sorted else None
-    plan = f3s.Plan(bsf, order, H=H, stream=stream)
+    plan = f3s.Plan(bsf, order, H=H, seg_tiles=args.seg, stream=stream)
     occ_sum, mask_bits = f3s.bsf_stats(bsf, masked, stream)
     dQ, dK, dV = (f3s.DeviceArray.from_numpy(x.view(np.uint16), stream) for x in (Q, K, V))
     dO = f3s.DeviceArray((n, H, d), np.float32)

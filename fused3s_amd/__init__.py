@@ -7,7 +7,8 @@ fused SDDMM -> online softmax -> SpMM pass -- behind the reference's host API
 graph.generate_balanced_window_order) and the C-ABI of libf3s_hip.so.
 Every compute call goes to the HIP library; there is no CPU fallback.
 """
-from .device import DeviceArray, Event, F3SError, Stream, device_count, device_name, synchronize
+from .device import (DeviceArray, Event, F3SError, Stream, device_count, device_name, init,
+                     synchronize)
 from .graph import (BlockSparseFormat, DeviceBSF, DeviceCSR, GraphData, bsf_stats,
                     convert_csr_to_block_sparse, convert_device, generate_balanced_window_order,
                     load_csr_graph, window_order_device)
@@ -15,7 +16,8 @@ from .attention import Plan, attention_fwd, cast_f32_to_f16
 from .configs import CONFIGS, Config
 
 __all__ = [
-    "DeviceArray", "Event", "F3SError", "Stream", "device_count", "device_name", "synchronize",
+    "DeviceArray", "Event", "F3SError", "Stream", "device_count", "device_name", "init",
+    "synchronize",
     "BlockSparseFormat", "DeviceBSF", "DeviceCSR", "GraphData", "bsf_stats",
     "convert_csr_to_block_sparse", "convert_device", "generate_balanced_window_order",
     "load_csr_graph", "window_order_device", "Plan", "attention_fwd", "cast_f32_to_f16",

@@ -24,6 +24,7 @@ HIP_API = {
     "f3s_status_string": (C.c_char_p, [c_i32]),
     "f3s_last_error": (C.c_char_p, []),
     "f3s_abi_version": (c_i32, []),
+    "f3s_init": (c_i32, []),
     "f3s_device_count": (c_i32, [P_i32]),
     "f3s_set_device": (c_i32, [c_i32]),
     "f3s_device_name": (c_i32, [C.c_char_p, c_i32]),

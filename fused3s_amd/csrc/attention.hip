@@ -14,11 +14,13 @@
 //
 // Work decomposition (one wave = one (item, head)):
 //   An item is a row window or, in a plan, a segment of a heavy window.
-//   The wave expands its tiles into a list of attended columns ("slots"),
-//   each with the mask of the window rows that attend it, held in a per-wave
-//   LDS ring: 64 tiles per step, one tile per lane, positions from a DPP
-//   wave prefix sum.  Columns no row attends are never gathered (column
-//   compaction).  Slots are consumed 32 at a time:
+//   MASKED: the wave expands its tiles into a list of attended columns
+//   ("slots"), each with the mask of the window rows that attend it, held in
+//   a per-wave LDS ring: 64 tiles per step, one tile per lane, positions from
+//   a DPP wave prefix sum.  Columns no row attends are never gathered (column
+//   compaction).  TILE_DENSE: a chunk is simply two whole tiles, i.e. 32
+//   columns in two runs of 16 contiguous K/V rows.  Slots are consumed 32 at
+//   a time (chunk_step):
 //     S^T[32 x 16] = K_slots[32 x 64] . Q_w^T    4 MFMA 16x16x32 (K gathered
 //                                                straight into A operands)
 //     masked online softmax, row r in lanes r, r+16, r+32, r+48
@@ -49,6 +51,7 @@ namespace f3s {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int kD = 64;             // feature dim per head (FEAT_DIM_FIXED, fused3s_v2.cu:41)
 constexpr int kRowBytes = kD * 2;  // one fp16 K/V/Q row of one head
@@ -71,8 +74,8 @@ struct SplitInfo {
 };
 
 struct __align__(16) WaveLds {
-    int32_t col[kRing];
-    uint32_t rm[kRing];
+    uint32_t off[kRing];   // byte offset of the slot's K/V row for this wave's head
+    uint32_t rm[kRing];    // rows of the window that attend the slot
     _Float16 v[kChunk * kD];
 };
 
@@ -153,9 +156,101 @@ __device__ __forceinline__ uint32_t column_rows(const uint32_t (&wd)[8], int c)
     return x;
 }
 
+// max over the lanes r, r+16, r+32, r+48 (the four lanes that hold row r),
+// with the gfx950 row and half-wave swaps (no LDS crossbar).
+__device__ __forceinline__ float row_max4(float x)
+{
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __builtin_fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __builtin_fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // Slot order of the 8 logits a lane holds (lane group g): S^T tile 0 rows
 // 4g..4g+3, then tile 1 rows 16+4g..16+4g+3.  Used as the k order of P.V.
 __device__ __forceinline__ int slot_of(int g, int j) { return (j < 4) ? 4 * g + j : 16 + 4 * g + (j - 4); }
+
+// Out-of-range buffer offset: loads read 0 (and a few added bytes cannot
+// wrap past 2^32, since the buffers are smaller than 2^32 - 512 bytes).
+constexpr uint32_t kNoRow = 0xffffff00u;
+
+// Online-softmax state of one row (lane (g, r) holds row r).  The running
+// max m (log2 domain) is moved only when a chunk's max exceeds it by more
+// than kLazy, so most chunks skip the rescale; weights exp2(x - m) then stay
+// <= 2^kLazy, well inside fp16 range, and numerator and denominator share m.
+struct RowState {
+    float m;
+    float l;        // this lane's share of the running sum of row r
+    f4 acc[4];      // O^T accumulators: dims 16g + 4v + t of row r (t = index, v = lane element)
+};
+constexpr float kLazy = 8.0f;
+
+// One chunk of 32 attended columns for the wave: S^T = K.Q^T, the masked
+// online-softmax update of row r, and O^T += V^T.P^T.  `valid` bit j says
+// whether the lane's j-th logit (slot slot_of(g, j)) is attended by row r.
+// vrow[i] holds 16 bytes of the V row of slot (lane >> 3) + 8i.
+__device__ __forceinline__ void chunk_step(RowState& st, const h8 (&ka)[2], const h8 (&kb)[2],
+                                           const h8 q0, const h8 q1, uint32_t valid,
+                                           const h8 (&vrow)[4], _Float16* __restrict__ vl,
+                                           int lane, float scale_log2)
+{
+    const int g = lane >> 4, r = lane & 15;
+    f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    s0 = mfma16x16x32(ka[0], q0, s0);
+    s0 = mfma16x16x32(ka[1], q1, s0);
+    s1 = mfma16x16x32(kb[0], q0, s1);
+    s1 = mfma16x16x32(kb[1], q1, s1);
+
+    float x[8];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        x[v] = ((valid >> v) & 1u) ? s0[v] * scale_log2 : -INFINITY;
+        x[4 + v] = ((valid >> (4 + v)) & 1u) ? s1[v] * scale_log2 : -INFINITY;
+    }
+    float cm = x[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) cm = __builtin_fmaxf(cm, x[j]);
+    cm = row_max4(cm);
+    if (__ballot(cm > st.m + kLazy)) {
+        if (cm > st.m + kLazy) {
+            const float corr = fast_exp2(st.m - cm);   // m = -inf -> 0
+            st.l *= corr;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) st.acc[t] *= corr;
+            st.m = cm;
+        }
+    }
+    const float mu = (st.m == -INFINITY) ? 0.f : st.m;
+    h8 pb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pb[j] = (_Float16)fast_exp2(x[j] - mu);
+    // the sum uses the rounded weights P.V uses
+    const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    st.l = __builtin_amdgcn_fdot2(h2{pb[0], pb[1]}, ones, st.l, false);
+    st.l = __builtin_amdgcn_fdot2(h2{pb[2], pb[3]}, ones, st.l, false);
+    st.l = __builtin_amdgcn_fdot2(h2{pb[4], pb[5]}, ones, st.l, false);
+    st.l = __builtin_amdgcn_fdot2(h2{pb[6], pb[7]}, ones, st.l, false);
+
+    // V through LDS, transposed into A operands
+    F3S_WAVE_LDS_SYNC();   // previous chunk's V reads are complete
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int s = (lane >> 3) + 8 * i;
+        *reinterpret_cast<h8*>(&vl[s * kD + 8 * (lane & 7)]) = vrow[i];
+    }
+    F3S_WAVE_LDS_SYNC();
+    h8 va[4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const h4 q = *reinterpret_cast<const h4*>(&vl[slot_of(g, j) * kD + 4 * r]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) va[t][j] = q[t];
+    }
+    // A row i of output tile t is dim 4i + t, so lane (g, r) holds dims
+    // 16g + 4v + t of row r.
+#pragma unroll
+    for (int t = 0; t < 4; ++t) st.acc[t] = mfma16x16x32(va[t], pb, st.acc[t]);
+}
 
 // WPG waves per workgroup; each wave processes one (item, head).  The
 // register budget is capped for 4 waves per SIMD.
@@ -168,7 +263,6 @@ fused_attention_kernel(const AttnParams p)
     const int lane = threadIdx.x % kWave;
     const int g = lane >> 4;                          // lane group
     const int r = lane & 15;                          // row of the window this lane owns
-    const int rbit = (r & 1) ? 16 + (r >> 1) : (r >> 1);   // row r in a ring row mask
     WaveLds& L = lds_all[wave];
 
     const int32_t n = p.n;
@@ -195,161 +289,137 @@ fused_attention_kernel(const AttnParams p)
     }
     const int32_t nbc = (n + 15) >> 4;   // valid block columns
     const int32_t* __restrict__ block_col = p.block_col;
-    const uint16_t* __restrict__ tile_mask = p.tile_mask;
     const __amdgpu_buffer_rsrc_t qres = make_rsrc(p.Q, p.feat_bytes);
     const __amdgpu_buffer_rsrc_t kres = make_rsrc(p.K, p.feat_bytes);
     const __amdgpu_buffer_rsrc_t vres = make_rsrc(p.V, p.feat_bytes);
     const uint32_t head_off = (uint32_t)h * kRowBytes;
-    constexpr uint32_t kNoRow = 0xfffffff0u;   // out of range (and no 32-bit wrap): loads return 0
+    const uint32_t row_stride = H * kRowBytes;
 
     // ---- Q tile in registers, B-operand layout ----
     const int32_t qrow = w * 16 + r;
-    const uint32_t qoff = qrow < n ? (uint32_t)qrow * (H * kRowBytes) + head_off + 16 * g : kNoRow;
+    const uint32_t qoff = qrow < n ? (uint32_t)qrow * row_stride + head_off + 16 * g : kNoRow;
     const h8 q0 = load_h8(qres, qoff);
-    const h8 q1 = load_h8(qres, qoff == kNoRow ? kNoRow : qoff + 64);
+    const h8 q1 = load_h8(qres, qoff + 64);
 
-    float m = -INFINITY;   // running max of row r (log2 domain)
-    float l = 0.f;         // this lane's share of the running sum of row r
-    f4 acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f},
-                 {0.f, 0.f, 0.f, 0.f}};
+    RowState st;
+    st.m = -INFINITY;
+    st.l = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) st.acc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
-    int32_t tcur = tb;
-    int32_t head = 0, tail = 0;   // ring positions (monotone, wave-uniform)
-    constexpr int32_t kMask = kRing - 1;
-
-    while (true) {
-        // ---- expand tiles into attended columns until a chunk is ready ----
-        while (tail - head < kChunk && tcur < te) {
-            const int32_t t = tcur + lane;
-            uint32_t u = 0;
-            int32_t bc = 0;
-            uint32_t wd[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (t < te) {
-                bc = block_col[t];
-                if ((uint32_t)bc < (uint32_t)nbc) {
-                    const int32_t left = n - bc * 16;
-                    const uint32_t valid = left >= 16 ? 0xffffu : ((1u << left) - 1u);
-                    if (MASKED) {
+    if constexpr (MASKED) {
+        // ---- column-compacted path: a ring of attended columns ----
+        const uint16_t* __restrict__ tile_mask = p.tile_mask;
+        const int rbit = (r & 1) ? 16 + (r >> 1) : (r >> 1);   // row r in a ring row mask
+        int32_t tcur = tb;
+        int32_t head = 0, tail = 0;   // ring positions (monotone, wave-uniform)
+        constexpr int32_t kMask = kRing - 1;
+        while (true) {
+            // expand tiles into attended columns until a chunk is ready
+            while (tail - head < kChunk && tcur < te) {
+                const int32_t t = tcur + lane;
+                uint32_t u = 0;
+                int32_t bc = 0;
+                uint32_t wd[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                if (t < te) {
+                    bc = block_col[t];
+                    if ((uint32_t)bc < (uint32_t)nbc) {
+                        const int32_t left = n - bc * 16;
+                        const uint32_t vmask = left >= 16 ? 0xffffu : ((1u << left) - 1u);
                         const uint4* mp = reinterpret_cast<const uint4*>(tile_mask + (int64_t)t * 16);
                         const uint4 a = mp[0], b = mp[1];
                         wd[0] = a.x; wd[1] = a.y; wd[2] = a.z; wd[3] = a.w;
                         wd[4] = b.x; wd[5] = b.y; wd[6] = b.z; wd[7] = b.w;
                         const uint32_t o = a.x | a.y | a.z | a.w | b.x | b.y | b.z | b.w;
-                        u = (o | (o >> 16)) & valid;
-                    } else {
-                        u = valid;
+                        u = (o | (o >> 16)) & vmask;
                     }
                 }
-            }
-            const int occ = __popc(u);
-            const int incl = wave_scan_incl(occ);
-            const int avail = kRing - (tail - head);
-            const bool accept = (t < te) && incl <= avail;
-            const int nacc = __popcll(__ballot(accept));          // accepted lanes: a prefix
-            const int added = __builtin_amdgcn_readlane(incl, nacc - 1);
-            if (accept && occ) {
-                int32_t pos = tail + incl - occ;
-                uint32_t rest = u;
-                while (rest) {
-                    const int c = __ffs(rest) - 1;
-                    rest &= rest - 1;
-                    L.col[pos & kMask] = bc * 16 + c;
-                    L.rm[pos & kMask] = MASKED ? column_rows(wd, c) : kAllRows;
-                    ++pos;
+                const int occ = __popc(u);
+                const int incl = wave_scan_incl(occ);
+                const int avail = kRing - kChunk - (tail - head);
+                const bool accept = (t < te) && incl <= avail;
+                const int nacc = __popcll(__ballot(accept));          // accepted lanes: a prefix
+                const int added = __builtin_amdgcn_readlane(incl, nacc - 1);
+                if (accept && occ) {
+                    int32_t pos = tail + incl - occ;
+                    const uint32_t base = (uint32_t)bc * 16 * row_stride + head_off;
+                    uint32_t rest = u;
+                    while (rest) {
+                        const int c = __ffs(rest) - 1;
+                        rest &= rest - 1;
+                        L.off[pos & kMask] = base + (uint32_t)c * row_stride;
+                        L.rm[pos & kMask] = column_rows(wd, c);
+                        ++pos;
+                    }
                 }
+                tail += added;
+                tcur += nacc;
             }
-            tail += added;
-            tcur += nacc;
+            const int32_t pending = tail - head;
+            if (pending <= 0) break;
+            if (pending < kChunk && lane < kChunk - pending) {
+                // last, partial chunk: pad with slots nobody attends, whose
+                // loads fall outside the buffers and read as zero
+                L.off[(tail + lane) & kMask] = kNoRow;
+                L.rm[(tail + lane) & kMask] = 0u;
+            }
+            F3S_WAVE_LDS_SYNC();
+            // Chunks start at multiples of 32 (only the last one is partial),
+            // so a chunk never wraps around the ring.
+            const uint32_t* off = &L.off[head & kMask];
+            const uint32_t* rmr = &L.rm[head & kMask];
+            const uint32_t o0 = off[r] + 16 * g, o1 = off[16 + r] + 16 * g;
+            const h8 ka[2] = {load_h8(kres, o0), load_h8(kres, o0 + 64)};
+            const h8 kb[2] = {load_h8(kres, o1), load_h8(kres, o1 + 64)};
+            h8 vrow[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                vrow[i] = load_h8(vres, off[(lane >> 3) + 8 * i] + 16 * (lane & 7));
+            const uint4 ra = *reinterpret_cast<const uint4*>(&rmr[4 * g]);
+            const uint4 rb = *reinterpret_cast<const uint4*>(&rmr[16 + 4 * g]);
+            const uint32_t valid =
+                ((ra.x >> rbit) & 1u) | (((ra.y >> rbit) & 1u) << 1) |
+                (((ra.z >> rbit) & 1u) << 2) | (((ra.w >> rbit) & 1u) << 3) |
+                (((rb.x >> rbit) & 1u) << 4) | (((rb.y >> rbit) & 1u) << 5) |
+                (((rb.z >> rbit) & 1u) << 6) | (((rb.w >> rbit) & 1u) << 7);
+            chunk_step(st, ka, kb, q0, q1, valid, vrow, L.v, lane, p.scale_log2);
+            head += pending < kChunk ? pending : kChunk;
         }
-        const int32_t pending = tail - head;
-        if (pending <= 0) break;
-        const int cnt = pending < kChunk ? pending : kChunk;
-        F3S_WAVE_LDS_SYNC();
-
-        // ---- gather K (A operands) and V (for LDS) of this chunk ----
-        auto row_off = [&](int s) -> uint32_t {
-            return s < cnt ? (uint32_t)L.col[(head + s) & kMask] * (H * kRowBytes) + head_off
-                           : kNoRow;
-        };
-        const uint32_t k0 = row_off(r), k1 = row_off(16 + r);
-        const h8 ka0 = load_h8(kres, k0 == kNoRow ? kNoRow : k0 + 16 * g);
-        const h8 ka1 = load_h8(kres, k0 == kNoRow ? kNoRow : k0 + 64 + 16 * g);
-        const h8 kb0 = load_h8(kres, k1 == kNoRow ? kNoRow : k1 + 16 * g);
-        const h8 kb1 = load_h8(kres, k1 == kNoRow ? kNoRow : k1 + 64 + 16 * g);
-        h8 vrow[4];
+    } else {
+        // ---- tile-dense path: two whole tiles (32 contiguous columns) per chunk ----
+        for (int32_t t = tb; t < te; t += 2) {
+            const int32_t bc0 = block_col[t];
+            const int32_t bc1 = (t + 1 < te) ? block_col[t + 1] : -1;
+            const bool ok0 = (uint32_t)bc0 < (uint32_t)nbc, ok1 = (uint32_t)bc1 < (uint32_t)nbc;
+            const int32_t c0 = 16 * bc0, c1 = 16 * bc1;
+            auto row_at = [&](bool ok, int32_t c, int s) -> uint32_t {
+                return ok && c + s < n ? (uint32_t)(c + s) * row_stride + head_off : kNoRow;
+            };
+            const uint32_t o0 = row_at(ok0, c0, r) + 16 * g, o1 = row_at(ok1, c1, r) + 16 * g;
+            const h8 ka[2] = {load_h8(kres, o0), load_h8(kres, o0 + 64)};
+            const h8 kb[2] = {load_h8(kres, o1), load_h8(kres, o1 + 64)};
+            h8 vrow[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t vo = row_off((lane >> 3) + 8 * i);
-            vrow[i] = load_h8(vres, vo == kNoRow ? kNoRow : vo + 16 * (lane & 7));
+            for (int i = 0; i < 4; ++i) {
+                const int s = (lane >> 3) + 8 * i;   // slots 0-15: tile t, 16-31: tile t+1
+                const uint32_t vo = s < 16 ? row_at(ok0, c0, s) : row_at(ok1, c1, s - 16);
+                vrow[i] = load_h8(vres, vo + 16 * (lane & 7));
+            }
+            // logit j of the lane is column 4g + j of tile t (j < 4) or
+            // 4g + j - 4 of tile t+1; attended iff the column exists
+            uint32_t valid = 0;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                valid |= (uint32_t)(ok0 && c0 + 4 * g + v < n) << v;
+                valid |= (uint32_t)(ok1 && c1 + 4 * g + v < n) << (4 + v);
+            }
+            chunk_step(st, ka, kb, q0, q1, valid, vrow, L.v, lane, p.scale_log2);
         }
-        uint32_t rmv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int s = slot_of(g, j);
-            rmv[j] = s < cnt ? L.rm[(head + s) & kMask] : 0u;
-        }
-
-        // ---- S^T = K . Q^T ----
-        f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-        s0 = mfma16x16x32(ka0, q0, s0);
-        s0 = mfma16x16x32(ka1, q1, s0);
-        s1 = mfma16x16x32(kb0, q0, s1);
-        s1 = mfma16x16x32(kb1, q1, s1);
-
-        // ---- masked online softmax for row r ----
-        float x[8];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            x[v] = ((rmv[v] >> rbit) & 1u) ? s0[v] * p.scale_log2 : -INFINITY;
-            x[4 + v] = ((rmv[4 + v] >> rbit) & 1u) ? s1[v] * p.scale_log2 : -INFINITY;
-        }
-        float cm = x[0];
-#pragma unroll
-        for (int j = 1; j < 8; ++j) cm = __builtin_fmaxf(cm, x[j]);
-        cm = __builtin_fmaxf(cm, __shfl_xor(cm, 16, kWave));
-        cm = __builtin_fmaxf(cm, __shfl_xor(cm, 32, kWave));
-        const float mn = __builtin_fmaxf(m, cm);
-        const float mu = (mn == -INFINITY) ? 0.f : mn;
-        const float corr = fast_exp2(m - mu);
-        h8 pb;
-        float ls = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const _Float16 pj = (_Float16)fast_exp2(x[j] - mu);
-            pb[j] = pj;
-            ls += (float)pj;   // the sum uses the rounded weights P.V uses
-        }
-        l = l * corr + ls;
-        m = mn;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] *= corr;
-
-        // ---- V through LDS, transposed into A operands ----
-        F3S_WAVE_LDS_SYNC();   // previous chunk's V reads are complete
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int s = (lane >> 3) + 8 * i;
-            *reinterpret_cast<h8*>(&L.v[s * kD + 8 * (lane & 7)]) = vrow[i];
-        }
-        F3S_WAVE_LDS_SYNC();
-        h8 va[4];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const h4 q = *reinterpret_cast<const h4*>(&L.v[slot_of(g, j) * kD + 4 * r]);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) va[t][j] = q[t];
-        }
-        // O^T rows for tile t are dims 4*i + t (i = A row): lane (g, r) ends up
-        // holding dims 16g + 4v + t of row r.
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] = mfma16x16x32(va[t], pb, acc[t]);
-
-        head += cnt;
     }
 
     // ---- epilogue ----
     const int32_t orow = w * 16 + r;
-    float lrow = l + __shfl_xor(l, 16, kWave);
+    float lrow = st.l + __shfl_xor(st.l, 16, kWave);
     lrow += __shfl_xor(lrow, 32, kWave);
     if (slot < 0) {
         const float inv = lrow > 0.f ? 1.0f / lrow : 0.f;
@@ -357,8 +427,8 @@ fused_attention_kernel(const AttnParams p)
             float* op = p.O + ((int64_t)orow * H + h) * kD + 16 * g;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                float4 o4 = make_float4(acc[0][v] * inv, acc[1][v] * inv, acc[2][v] * inv,
-                                        acc[3][v] * inv);
+                float4 o4 = make_float4(st.acc[0][v] * inv, st.acc[1][v] * inv, st.acc[2][v] * inv,
+                                        st.acc[3][v] * inv);
                 *reinterpret_cast<float4*>(op + 4 * v) = o4;
             }
         }
@@ -370,9 +440,9 @@ fused_attention_kernel(const AttnParams p)
 #pragma unroll
     for (int v = 0; v < 4; ++v)
         *reinterpret_cast<float4*>(op + 4 * v) =
-            make_float4(acc[0][v], acc[1][v], acc[2][v], acc[3][v]);
+            make_float4(st.acc[0][v], st.acc[1][v], st.acc[2][v], st.acc[3][v]);
     if (g == 0) {
-        part[16 * kD + r] = m;
+        part[16 * kD + r] = st.m;
         part[16 * kD + 16 + r] = lrow;
     }
 }
@@ -423,6 +493,14 @@ __global__ void __launch_bounds__(256) merge_partials_kernel(const AttnParams p)
             *reinterpret_cast<float4*>(dst + 4 * v) =
                 make_float4(o[v].x * inv, o[v].y * inv, o[v].z * inv, o[v].w * inv);
     }
+}
+
+__global__ void warm_attention_kernel() {}
+
+hipError_t warm_attention(hipStream_t s)
+{
+    hipLaunchKernelGGL(warm_attention_kernel, dim3(1), dim3(64), 0, s);
+    return hipGetLastError();
 }
 
 // ----------------------------------------------------------------- planner
@@ -501,7 +579,7 @@ static f3s_status check_attention_args(const void* Q, const void* K, const void*
     F3S_REQUIRE(n == 0 || (Q && K && V && O), "attention: NULL feature pointer");
     F3S_REQUIRE(((((uintptr_t)Q) | ((uintptr_t)K) | ((uintptr_t)V) | ((uintptr_t)O)) & 15) == 0,
                 "attention: Q, K, V, O must be 16-byte aligned");
-    if ((int64_t)n * H * kRowBytes >= ((int64_t)1 << 32) - 64) {
+    if ((int64_t)n * H * kRowBytes >= ((int64_t)1 << 32) - 512) {
         set_error("attention: Q/K/V larger than 4 GiB are not supported (32-bit buffer offsets)");
         return F3S_EUNSUPPORTED;
     }
@@ -613,8 +691,10 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     // small fraction of one wave slot's share of the whole pass.
     int64_t seg = seg_tiles;
     if (seg == 0) {
+        // Small graphs are not split: a merge launch costs more than the
+        // serial tail it removes.
         seg = ceil_div(p->T * H, 8192);
-        if (seg < 16) seg = 16;
+        if (seg < 256) seg = 256;
     }
     if (seg > INT32_MAX) seg = INT32_MAX;
     p->seg = (int32_t)seg;

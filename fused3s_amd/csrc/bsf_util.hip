@@ -56,6 +56,14 @@ bsf_stats_kernel(const int32_t* __restrict__ block_col, const uint16_t* __restri
     }
 }
 
+__global__ void warm_bsf_util_kernel() {}
+
+hipError_t warm_bsf_util(hipStream_t s)
+{
+    hipLaunchKernelGGL(warm_bsf_util_kernel, dim3(1), dim3(64), 0, s);
+    return hipGetLastError();
+}
+
 }  // namespace f3s
 
 using namespace f3s;

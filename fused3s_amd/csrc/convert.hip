@@ -337,6 +337,14 @@ static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, i
     return F3S_OK;
 }
 
+__global__ void warm_convert_kernel() {}
+
+hipError_t warm_convert(hipStream_t s)
+{
+    hipLaunchKernelGGL(warm_convert_kernel, dim3(1), dim3(64), 0, s);
+    return hipGetLastError();
+}
+
 }  // namespace f3s
 
 extern "C" f3s_status f3s_convert_csr_to_bsf(const int32_t* d_row_ptr, const int32_t* d_col_idx,

@@ -32,6 +32,13 @@ int64_t scan_tmp_elems(int64_t count);
 f3s_status exclusive_scan_i32_to_i64(const int32_t* in, int64_t* out, int64_t count,
                                      int64_t* tmp, hipStream_t stream);
 
+// Each translation unit's code object is loaded onto the device at its
+// first kernel launch; these launch one empty kernel per unit (f3s_init).
+hipError_t warm_runtime(hipStream_t s);
+hipError_t warm_convert(hipStream_t s);
+hipError_t warm_attention(hipStream_t s);
+hipError_t warm_bsf_util(hipStream_t s);
+
 // Small grow-only device buffer (per call site).
 struct DeviceBuffer {
     void* ptr = nullptr;

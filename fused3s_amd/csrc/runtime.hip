@@ -152,6 +152,14 @@ cast_f32_to_f16_kernel(const float* __restrict__ in, _Float16* __restrict__ out,
     }
 }
 
+__global__ void warm_runtime_kernel() {}
+
+hipError_t warm_runtime(hipStream_t s)
+{
+    hipLaunchKernelGGL(warm_runtime_kernel, dim3(1), dim3(64), 0, s);
+    return hipGetLastError();
+}
+
 }  // namespace f3s
 
 using namespace f3s;
@@ -175,6 +183,17 @@ const char* f3s_status_string(f3s_status s)
 const char* f3s_last_error(void) { return g_last_error.c_str(); }
 
 int32_t f3s_abi_version(void) { return F3S_ABI_VERSION; }
+
+f3s_status f3s_init(void)
+{
+    F3S_TRY(require_device());
+    F3S_HIP(warm_runtime(nullptr));
+    F3S_HIP(warm_convert(nullptr));
+    F3S_HIP(warm_attention(nullptr));
+    F3S_HIP(warm_bsf_util(nullptr));
+    F3S_HIP(hipDeviceSynchronize());
+    return F3S_OK;
+}
 
 f3s_status f3s_device_count(int32_t* count)
 {

@@ -34,6 +34,11 @@ def device_count() -> int:
     return int(n.value)
 
 
+def init() -> None:
+    """Loads the library's GPU code now (f3s_init) instead of at first launch."""
+    check(_lib.hip().f3s_init(), "f3s_init")
+
+
 def device_name() -> str:
     buf = C.create_string_buffer(256)
     check(_lib.hip().f3s_device_name(buf, 256), "f3s_device_name")

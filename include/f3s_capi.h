@@ -20,8 +20,9 @@
  *                  style buffer padded to 16W rows also works).
  *
  * Thread safety: calls on different streams may run concurrently; the
- * library keeps no mutable global state besides the per-thread last error
- * and the per-device scratch of the planned path (documented there).
+ * library keeps no mutable global state besides the per-thread last error.
+ * A plan owns the partial-result buffers of its split windows, so one plan
+ * must not serve two overlapping calls.
  */
 #ifndef F3S_CAPI_H
 #define F3S_CAPI_H
@@ -52,6 +53,12 @@ typedef int32_t f3s_status;
 const char* f3s_status_string(f3s_status s);
 const char* f3s_last_error(void);
 int32_t f3s_abi_version(void);
+
+/* Loads the library's GPU code onto the current device now rather than at
+ * the first launch of each kernel (HIP loads code objects lazily), so the
+ * first timed call is not charged for it.  Optional; idempotent.  The
+ * reference has no counterpart (CUDA contexts load modules the same way). */
+f3s_status f3s_init(void);
 
 /* ---- device plumbing (replaces the CUDA_CHECK'ed runtime calls of the
  *      reference harness, tests/test_fused_3s_v2.cu:93-120,139,157-159) ---- */
@@ -116,11 +123,14 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
 
 /* Planned execution (no reference counterpart; the reference relies on the
  * window sort alone, include/utils.cuh:48-59).  A plan splits windows with
- * more than `seg_tiles` tiles (0 = automatic) into segments processed by
- * separate waves and merged inside the same kernel launch, so hub windows do
- * not serialise.  Build once per graph; reuse for every forward pass.
- * A plan must not be used by two overlapping calls (it owns the merge
- * counters). */
+ * more than `seg_tiles` tiles (0 = automatic: none on small graphs) into
+ * segments processed by separate waves; a second, small launch merges each
+ * split window's segments in a fixed order (deterministic), so hub windows do
+ * not serialise.  Windows run in d_window_order (the reference's descending
+ * sort) or, when it is NULL, in natural order with consecutive windows kept
+ * on one XCD (for community-ordered graphs).  Build once per graph; reuse for
+ * every forward pass; one plan must not serve two overlapping calls (it owns
+ * the partial-result buffers). */
 typedef struct f3s_plan f3s_plan;
 f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_window_order,
                            int32_t W, int32_t H, int32_t seg_tiles, void* stream,
