@@ -86,6 +86,9 @@ def main() -> int:
                          "auto = natural for the community-ordered SBM config, else sorted")
     ap.add_argument("--seg", type=int, default=0,
                     help="plan segment size in tiles (0 = automatic)")
+    ap.add_argument("--no-compile", action="store_true",
+                    help="masked passes expand tiles on every pass instead of using the "
+                         "plan's compiled column lists")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run device-to-device copies of this size (calibrates the "
@@ -134,12 +137,18 @@ def main() -> int:
     conv_ms = ev0.elapsed_ms(ev1)
     use_sorted = args.order == "sorted" or (args.order == "auto" and c.kind != "sbm")
     order = f3s.window_order_device(bsf, stream) if use_sorted else None
+    ev0.record(stream)
     plan = f3s.Plan(bsf, order, H=H, seg_tiles=args.seg, stream=stream)
+    if masked and not args.no_compile:
+        plan.compile(stream)
+    ev1.record(stream)
+    plan_ms = ev0.elapsed_ms(ev1)
     occ_sum, mask_bits = f3s.bsf_stats(bsf, masked, stream)
     dQ, dK, dV = (f3s.DeviceArray.from_numpy(x.view(np.uint16), stream) for x in (Q, K, V))
     dO = f3s.DeviceArray((n, H, d), np.float32)
     print(f"[bench] W={bsf.W} T={bsf.T} occ={occ_sum} items={plan.num_items} "
-          f"split={plan.num_split} seg={plan.seg_tiles} convert={conv_ms:.2f}ms",
+          f"split={plan.num_split} seg={plan.seg_tiles} convert={conv_ms:.2f}ms "
+          f"plan={plan_ms:.2f}ms",
           file=sys.stderr, flush=True)
 
     # cold first launch (the reference times exactly this, tests/test_fused_3s_v2.cu:126-137)
@@ -197,6 +206,8 @@ def main() -> int:
         "alg_bytes_per_launch": nbytes,
         "mfma_frac_tile_model": flops_tile / (kavg * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
         "converter_us": conv_ms * 1e3,
+        "plan_us": plan_ms * 1e3,
+        "plan_compiled": bool(masked and not args.no_compile),
         "device": f3s.device_name(),
     }
     if not args.no_cpu_baseline:

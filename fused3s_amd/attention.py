@@ -46,6 +46,15 @@ class Plan:
                                        C.byref(seg)), "f3s_plan_info")
         self.num_items, self.num_split, self.T, self.seg_tiles = ni.value, ns.value, T.value, seg.value
 
+    def compile(self, stream: Stream | None = None) -> None:
+        """f3s_plan_compile: list the attended columns once (masked passes)."""
+        bsf = self.bsf
+        if bsf.tile_mask is None:
+            raise ValueError("compiling a plan needs a BSF converted with masks")
+        check(_lib.hip().f3s_plan_compile(self.handle, bsf.block_col.ptr, bsf.tile_mask.ptr,
+                                          bsf.n, stream.handle if stream else None),
+              "f3s_plan_compile")
+
     def forward(self, Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray,
                 masked: bool = True, d: int = 64, scale: float = 1.0,
                 stream: Stream | None = None) -> None:

@@ -97,6 +97,8 @@ struct AttnParams {
     float* partials;
     const SplitInfo* splits;
     int64_t num_split;
+    const int32_t* chunk_base;       // compiled plan: item i owns chunks [cb[i], cb[i+1])
+    const uint32_t* columns;         // compiled plan: per chunk 32 row offsets, 32 row masks
 };
 
 // Workgroup index -> logical block.  The dispatcher deals workgroups to the
@@ -308,6 +310,43 @@ fused_attention_kernel(const AttnParams p)
     for (int t = 0; t < 4; ++t) st.acc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
     if constexpr (MASKED) {
+      if (p.chunk_base) {
+        // ---- compiled plan: the attended columns were listed once per graph ----
+        const int rbit = (r & 1) ? 16 + (r >> 1) : (r >> 1);
+        const int64_t cb = p.chunk_base[item_idx], ce = p.chunk_base[item_idx + 1];
+        const uint32_t add = head_off + 16 * g;
+        uint32_t mk0 = 0, mk1 = 0, mv[4] = {0, 0, 0, 0};
+        uint4 mra = make_uint4(0, 0, 0, 0), mrb = make_uint4(0, 0, 0, 0);
+        auto load_meta = [&](int64_t c) {
+            const uint32_t* rec = p.columns + c * 64;
+            mk0 = rec[r];
+            mk1 = rec[16 + r];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mv[i] = rec[(lane >> 3) + 8 * i];
+            mra = *reinterpret_cast<const uint4*>(rec + 32 + 4 * g);
+            mrb = *reinterpret_cast<const uint4*>(rec + 48 + 4 * g);
+        };
+        if (cb < ce) load_meta(cb);
+        for (int64_t c = cb; c < ce; ++c) {
+            const uint32_t o0 = mk0 + add, o1 = mk1 + add;
+            uint32_t vo[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vo[i] = mv[i] + head_off + 16 * (lane & 7);
+            const uint4 ra = mra, rb = mrb;
+            if (c + 1 < ce) load_meta(c + 1);   // next chunk's list, while this one runs
+            const h8 ka[2] = {load_h8(kres, o0), load_h8(kres, o0 + 64)};
+            const h8 kb[2] = {load_h8(kres, o1), load_h8(kres, o1 + 64)};
+            h8 vrow[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vrow[i] = load_h8(vres, vo[i]);
+            const uint32_t valid =
+                ((ra.x >> rbit) & 1u) | (((ra.y >> rbit) & 1u) << 1) |
+                (((ra.z >> rbit) & 1u) << 2) | (((ra.w >> rbit) & 1u) << 3) |
+                (((rb.x >> rbit) & 1u) << 4) | (((rb.y >> rbit) & 1u) << 5) |
+                (((rb.z >> rbit) & 1u) << 6) | (((rb.w >> rbit) & 1u) << 7);
+            chunk_step(st, ka, kb, q0, q1, valid, vrow, L.v, lane, p.scale_log2);
+        }
+      } else {
         // ---- column-compacted path: a ring of attended columns ----
         const uint16_t* __restrict__ tile_mask = p.tile_mask;
         const int rbit = (r & 1) ? 16 + (r >> 1) : (r >> 1);   // row r in a ring row mask
@@ -385,6 +424,7 @@ fused_attention_kernel(const AttnParams p)
             chunk_step(st, ka, kb, q0, q1, valid, vrow, L.v, lane, p.scale_log2);
             head += pending < kChunk ? pending : kChunk;
         }
+      }
     } else {
         // ---- tile-dense path: two whole tiles (32 contiguous columns) per chunk ----
         for (int32_t t = tb; t < te; t += 2) {
@@ -553,6 +593,79 @@ __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __res
     }
 }
 
+__global__ void offsets_to_i32_plan(const int64_t* __restrict__ in, int32_t* __restrict__ out,
+                                    int64_t count)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) out[i] = (int32_t)in[i];
+}
+
+// Attended columns of each planned item (masked semantics): one wave per
+// item counts them (pass 1) or lists them, in tile order, padded to whole
+// chunks (pass 2) -- the expansion the ring path performs on every pass,
+// done once per graph.
+template <bool FILL>
+__global__ void __launch_bounds__(256)
+plan_columns(const Item* __restrict__ items, int64_t num_items,
+             const int32_t* __restrict__ block_col, const uint16_t* __restrict__ tile_mask,
+             int32_t n, uint32_t row_stride, int32_t* __restrict__ nchunks,
+             const int64_t* __restrict__ chunk_base, uint32_t* __restrict__ columns)
+{
+    const int64_t it = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (it >= num_items) return;
+    const Item item = items[it];
+    const int32_t nbc = (n + 15) >> 4;
+    int64_t pos = 0;   // wave-uniform
+    uint32_t* rec0 = FILL ? columns + chunk_base[it] * 64 : nullptr;
+    for (int32_t t0 = item.tb; t0 < item.te; t0 += kWave) {
+        const int32_t t = t0 + lane;
+        uint32_t u = 0;
+        int32_t bc = 0;
+        uint32_t wd[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (t < item.te) {
+            bc = block_col[t];
+            if ((uint32_t)bc < (uint32_t)nbc) {
+                const int32_t left = n - bc * 16;
+                const uint32_t vmask = left >= 16 ? 0xffffu : ((1u << left) - 1u);
+                const uint4* mp = reinterpret_cast<const uint4*>(tile_mask + (int64_t)t * 16);
+                const uint4 a = mp[0], b = mp[1];
+                wd[0] = a.x; wd[1] = a.y; wd[2] = a.z; wd[3] = a.w;
+                wd[4] = b.x; wd[5] = b.y; wd[6] = b.z; wd[7] = b.w;
+                const uint32_t o = a.x | a.y | a.z | a.w | b.x | b.y | b.z | b.w;
+                u = (o | (o >> 16)) & vmask;
+            }
+        }
+        const int occ = __popc(u);
+        const int incl = wave_scan_incl(occ);
+        if (FILL && occ) {
+            int64_t q = pos + incl - occ;
+            const uint32_t base = (uint32_t)bc * 16 * row_stride;
+            uint32_t rest = u;
+            while (rest) {
+                const int c = __ffs(rest) - 1;
+                rest &= rest - 1;
+                uint32_t* rec = rec0 + (q >> 5) * 64;
+                rec[q & 31] = base + (uint32_t)c * row_stride;
+                rec[32 + (q & 31)] = column_rows(wd, c);
+                ++q;
+            }
+        }
+        pos += __builtin_amdgcn_readlane(incl, kWave - 1);
+    }
+    const int64_t nch = (pos + kChunk - 1) / kChunk;
+    if (!FILL) {
+        if (lane == 0) nchunks[it] = (int32_t)nch;
+        return;
+    }
+    // pad the last chunk with slots no row attends, read as zero
+    for (int64_t q = pos + lane; q < nch * kChunk; q += kWave) {
+        uint32_t* rec = rec0 + (q >> 5) * 64;
+        rec[q & 31] = kNoRow;
+        rec[32 + (q & 31)] = 0u;
+    }
+}
+
 }  // namespace f3s
 
 struct f3s_plan {
@@ -560,6 +673,12 @@ struct f3s_plan {
     int32_t natural_order = 1;   // no window order given: keep neighbours on one XCD
     int64_t T = 0, num_items = 0, num_split = 0, num_slots = 0;
     f3s::DeviceBuffer items, splits, partials;
+    // compiled column lists (f3s_plan_compile) and the structure they describe
+    f3s::DeviceBuffer chunk_base, columns;
+    const int32_t* compiled_block_col = nullptr;
+    const uint16_t* compiled_tile_mask = nullptr;
+    int32_t compiled_n = -1;
+    int64_t num_chunks = 0;
 };
 
 namespace f3s {
@@ -756,6 +875,65 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     return F3S_OK;
 }
 
+f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
+                            const uint16_t* d_tile_mask, int32_t n, void* stream)
+{
+    F3S_REQUIRE(plan != nullptr, "f3s_plan_compile: NULL plan");
+    F3S_REQUIRE(d_tile_mask != nullptr, "f3s_plan_compile: needs the tile masks");
+    F3S_REQUIRE(plan->T == 0 || d_block_col, "f3s_plan_compile: NULL block_col");
+    F3S_REQUIRE((((uintptr_t)d_tile_mask) & 15) == 0, "f3s_plan_compile: tile_mask alignment");
+    F3S_REQUIRE(plan->W == (int32_t)ceil_div(n, 16), "f3s_plan_compile: n does not match W");
+    F3S_REQUIRE((int64_t)n * plan->H * kRowBytes < ((int64_t)1 << 32) - 512,
+                "f3s_plan_compile: features larger than 4 GiB");
+    F3S_TRY(require_device());
+    clear_error();
+    hipStream_t st = as_stream(stream);
+    plan->compiled_tile_mask = nullptr;
+    plan->compiled_block_col = nullptr;
+    plan->compiled_n = -1;
+    const int64_t ni = plan->num_items;
+    DeviceBuffer counts, tmp;
+    F3S_TRY(counts.reserve(sizeof(int32_t) * (size_t)(ni + 1)));
+    F3S_TRY(tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(ni)));
+    DeviceBuffer base64;
+    F3S_TRY(base64.reserve(sizeof(int64_t) * (size_t)(ni + 1)));
+    const uint32_t row_stride = (uint32_t)plan->H * kRowBytes;
+    const auto* items = reinterpret_cast<const Item*>(plan->items.ptr);
+    const dim3 grid((unsigned)ceil_div(ni > 0 ? ni : 1, 4));
+    if (ni > 0)
+        hipLaunchKernelGGL(plan_columns<false>, grid, dim3(256), 0, st, items, ni, d_block_col,
+                           d_tile_mask, n, row_stride, reinterpret_cast<int32_t*>(counts.ptr),
+                           nullptr, nullptr);
+    F3S_HIP(hipGetLastError());
+    auto* b64 = reinterpret_cast<int64_t*>(base64.ptr);
+    F3S_TRY(exclusive_scan_i32_to_i64(reinterpret_cast<const int32_t*>(counts.ptr), b64, ni,
+                                      reinterpret_cast<int64_t*>(tmp.ptr), st));
+    int64_t total = 0;
+    F3S_HIP(hipMemcpyAsync(&total, b64 + ni, sizeof total, hipMemcpyDeviceToHost, st));
+    F3S_HIP(hipStreamSynchronize(st));
+    if (total >= INT32_MAX) {
+        set_error("f3s_plan_compile: more than 2^31-1 chunks");
+        return F3S_EUNSUPPORTED;
+    }
+    F3S_TRY(plan->columns.reserve(sizeof(uint32_t) * 64 * (size_t)(total > 0 ? total : 1)));
+    F3S_TRY(plan->chunk_base.reserve(sizeof(int32_t) * (size_t)(ni + 1)));
+    if (ni > 0) {
+        hipLaunchKernelGGL(plan_columns<true>, grid, dim3(256), 0, st, items, ni, d_block_col,
+                           d_tile_mask, n, row_stride, nullptr, b64,
+                           reinterpret_cast<uint32_t*>(plan->columns.ptr));
+        F3S_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(offsets_to_i32_plan, dim3((unsigned)ceil_div(ni + 1, 256)), dim3(256), 0,
+                       st, b64, reinterpret_cast<int32_t*>(plan->chunk_base.ptr), ni + 1);
+    F3S_HIP(hipGetLastError());
+    F3S_HIP(hipStreamSynchronize(st));
+    plan->num_chunks = total;
+    plan->compiled_tile_mask = d_tile_mask;
+    plan->compiled_block_col = d_block_col;
+    plan->compiled_n = n;
+    return F3S_OK;
+}
+
 f3s_status f3s_plan_destroy(f3s_plan* plan)
 {
     delete plan;
@@ -803,6 +981,11 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
     p.partials = reinterpret_cast<float*>(plan->partials.ptr);
     p.splits = reinterpret_cast<const SplitInfo*>(plan->splits.ptr);
     p.num_split = plan->num_split;
+    if (d_tile_mask && d_tile_mask == plan->compiled_tile_mask &&
+        d_block_col == plan->compiled_block_col && n == plan->compiled_n) {
+        p.chunk_base = reinterpret_cast<const int32_t*>(plan->chunk_base.ptr);
+        p.columns = reinterpret_cast<const uint32_t*>(plan->columns.ptr);
+    }
     return launch(p, H, scale, as_stream(stream));
 }
 

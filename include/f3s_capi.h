@@ -136,6 +136,15 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
                            int32_t W, int32_t H, int32_t seg_tiles, void* stream,
                            f3s_plan** plan_out);
 f3s_status f3s_plan_destroy(f3s_plan* plan);
+/* Lists, once per graph, the columns each planned item attends under the
+ * masked semantics (32 row offsets + 32 row masks per 32-column chunk), so
+ * masked passes read 8 bytes per attended column instead of expanding 36
+ * bytes of tile metadata on every pass.  Later masked calls of
+ * f3s_attention_fwd_planned with these same d_block_col / d_tile_mask
+ * pointers and n use the lists; the structure they point to must not change
+ * afterwards (compile again if it does).  Other calls are unaffected. */
+f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
+                            const uint16_t* d_tile_mask, int32_t n, void* stream);
 f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_split_windows,
                          int64_t* T, int32_t* seg_tiles);
 f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q,

@@ -69,10 +69,12 @@ class Problem:
     def host_bsf(self):
         return self.bsf.to_host()
 
-    def run(self, masked=True, planned=False, seg=0, order=None, scale=1.0):
+    def run(self, masked=True, planned=False, seg=0, order=None, scale=1.0, compiled=False):
         self.dO.fill_bytes(0xFF)    # NaN poison: every real row must be written
         if planned:
             plan = self.f3s.Plan(self.bsf, order, H=self.H, seg_tiles=seg)
+            if compiled:
+                plan.compile()
             plan.forward(self.dQ, self.dK, self.dV, self.dO, masked=masked, scale=scale)
         else:
             self.f3s.attention_fwd(self.dQ, self.dK, self.dV, self.dO, self.bsf, order,
@@ -239,9 +241,9 @@ def test_attention_fixtures(gpu, name, masked):
     g = gpu.load_csr_graph(str(GOLDEN / name))
     p = Problem(gpu, g.row_ptr, g.col_ind, seed=1)
     want = p.oracle(masked)
-    for planned in (False, True):
-        got = p.run(masked, planned=planned, seg=16)
-        assert_close(got, want, f"{name} masked={masked} planned={planned}")
+    for planned, compiled in ((False, False), (True, False), (True, True)):
+        got = p.run(masked, planned=planned, seg=16, compiled=compiled and masked)
+        assert_close(got, want, f"{name} masked={masked} planned={planned} compiled={compiled}")
 
 
 @pytest.mark.parametrize("cfg", [2, 3])
@@ -252,9 +254,11 @@ def test_attention_configs_small(gpu, cfg, masked):
     p = Problem(gpu, rp, ci, H=c.H, normal=c.normal, seed=cfg)
     want = p.oracle(masked)
     order = gpu.window_order_device(p.bsf)
-    for planned, seg in ((False, 0), (True, 0), (True, 8)):
-        got = p.run(masked, planned=planned, seg=seg, order=order)
-        assert_close(got, want, f"cfg{cfg} masked={masked} planned={planned} seg={seg}")
+    for planned, seg, compiled in ((False, 0, False), (True, 0, False), (True, 8, False),
+                                   (True, 0, True), (True, 8, True)):
+        got = p.run(masked, planned=planned, seg=seg, order=order, compiled=compiled and masked)
+        assert_close(got, want, f"cfg{cfg} masked={masked} planned={planned} seg={seg} "
+                                f"compiled={compiled}")
 
 
 @pytest.mark.parametrize("H", [1, 2, 4])
@@ -264,9 +268,10 @@ def test_attention_random_heads(gpu, H, n, deg, seed):
     p = Problem(gpu, rp, ci, H=H, normal=True, seed=seed)
     for masked in (True, False):
         want = p.oracle(masked, scale=0.125)
-        for planned in (False, True):
-            got = p.run(masked, planned=planned, seg=4, scale=0.125)
-            assert_close(got, want, f"n={n} H={H} masked={masked} planned={planned}")
+        for planned, compiled in ((False, False), (True, False), (True, True)):
+            got = p.run(masked, planned=planned, seg=4, scale=0.125, compiled=compiled and masked)
+            assert_close(got, want, f"n={n} H={H} masked={masked} planned={planned} "
+                                    f"compiled={compiled}")
 
 
 def test_attention_hub_split_merge(gpu):
@@ -274,8 +279,9 @@ def test_attention_hub_split_merge(gpu):
     p = Problem(gpu, rp, ci, H=1, normal=True, seed=9)
     want = p.oracle(True)
     for seg in (0, 64, 1000):
-        got = p.run(True, planned=True, seg=seg)
-        assert_close(got, want, f"star seg={seg}")
+        for compiled in (False, True):
+            got = p.run(True, planned=True, seg=seg, compiled=compiled)
+            assert_close(got, want, f"star seg={seg} compiled={compiled}")
     got = p.run(True, planned=False)
     assert_close(got, want, "star unplanned")
 
@@ -305,6 +311,11 @@ def test_attention_deterministic(gpu):
     a = p.run(True, planned=True, seg=32)
     b = p.run(True, planned=True, seg=32)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    c = p.run(True, planned=True, seg=32, compiled=True)
+    d = p.run(True, planned=True, seg=32, compiled=True)
+    assert np.array_equal(c.view(np.uint32), d.view(np.uint32))
+    # the compiled list visits the columns in the ring's order: same bits
+    assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
 
 
 def test_attention_rejects_bad_args(gpu):
@@ -349,9 +360,11 @@ def test_config4_full_size(gpu):
     ranges = sample_rows(hb, n)
     plan = gpu.Plan(bsf, order, H=1)
     log(f"cfg4 plan: items={plan.num_items} split={plan.num_split} seg={plan.seg_tiles}")
-    for masked in (True, False):
+    cplan = gpu.Plan(bsf, order, H=1)
+    cplan.compile()
+    for masked, pl in ((True, plan), (True, cplan), (False, plan)):
         dO.fill_bytes(0xFF)
-        plan.forward(dQ, dK, dV, dO, masked=masked)
+        pl.forward(dQ, dK, dV, dO, masked=masked)
         gpu.synchronize()
         got = dO.numpy()
         assert np.all(np.isfinite(got)), "unwritten or non-finite rows"
@@ -385,6 +398,7 @@ def test_config5_full_size(gpu):
     # oracle inputs restricted to the rows needed (sampled rows + neighbours)
     Qf, Kf, Vf = (x.astype(np.float32) for x in (Q, K, V))
     plan = gpu.Plan(bsf, None, H=H)
+    plan.compile()
     dO.fill_bytes(0xFF)
     plan.forward(dQ, dK, dV, dO, masked=True)
     gpu.synchronize()
