@@ -12,7 +12,7 @@ from .device import (DeviceArray, Event, F3SError, Stream, device_count, device_
 from .graph import (BlockSparseFormat, DeviceBSF, DeviceCSR, GraphData, bsf_stats,
                     convert_csr_to_block_sparse, convert_device, generate_balanced_window_order,
                     load_csr_graph, window_order_device)
-from .attention import Plan, attention_fwd, cast_f32_to_f16
+from .attention import Plan, attention_fwd, cast_f32_to_f16, naive_attention_fwd
 from .configs import CONFIGS, Config
 
 __all__ = [
@@ -21,5 +21,6 @@ __all__ = [
     "BlockSparseFormat", "DeviceBSF", "DeviceCSR", "GraphData", "bsf_stats",
     "convert_csr_to_block_sparse", "convert_device", "generate_balanced_window_order",
     "load_csr_graph", "window_order_device", "Plan", "attention_fwd", "cast_f32_to_f16",
+    "naive_attention_fwd",
     "CONFIGS", "Config",
 ]

@@ -81,3 +81,14 @@ def cast_f32_to_f16(x: DeviceArray, out: DeviceArray, stream: Stream | None = No
     count = int(np.prod(x.shape))
     check(_lib.hip().f3s_cast_f32_to_f16(x.ptr, out.ptr, count, stream.handle if stream else None),
           "f3s_cast_f32_to_f16")
+
+
+def naive_attention_fwd(Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray,
+                        csr, d: int = 64, scale: float = 1.0,
+                        stream: Stream | None = None) -> None:
+    """f3s_naive_attention_fwd: the naive edge-exact comparator
+    (baselines/gpu_baseline.cu:28-116), fp32 [n][d] features, CSR as stored."""
+    check(_lib.hip().f3s_naive_attention_fwd(Q.ptr, K.ptr, V.ptr, O.ptr, csr.row_ptr.ptr,
+                                             csr.col_idx.ptr, csr.n, d, scale,
+                                             stream.handle if stream else None),
+          "f3s_naive_attention_fwd")

@@ -23,7 +23,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
-HIP_SOURCES = ["runtime.hip", "convert.hip", "attention.hip", "bsf_util.hip"]
+HIP_SOURCES = ["runtime.hip", "convert.hip", "attention.hip", "bsf_util.hip", "naive.hip"]
 HOST_SOURCES = ["host/gen.cpp", "host/graph.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -84,13 +84,26 @@ def build_oracle(verbose: bool = True) -> None:
     _run(["make", "-s", "-C", str(ROOT / "oracle")], verbose)
 
 
-def build_harness(verbose: bool = True) -> Path | None:
-    src = ROOT / "tests" / "cpp" / "test_fused_3s.cpp"
+HARNESSES = ["test_fused_3s", "test_baselines"]
+
+
+def build_harness(verbose: bool = True) -> list[Path]:
+    """The C++ harness binaries (tests/cpp/*.cpp); they link the oracle."""
+    outs = []
+    for name in HARNESSES:
+        out = _build_one_harness(name, verbose)
+        if out:
+            outs.append(out)
+    return outs
+
+
+def _build_one_harness(name: str, verbose: bool) -> Path | None:
+    src = ROOT / "tests" / "cpp" / f"{name}.cpp"
     if not src.exists() or not (ROOT / "oracle" / "liboracle.so").exists():
         return None
     bindir = ROOT / "tests" / "cpp" / "bin"
     bindir.mkdir(parents=True, exist_ok=True)
-    out = bindir / "test_fused_3s"
+    out = bindir / name
     cmd = ["g++", "-O2", "-std=c++17", "-fopenmp", "-Wall", str(src),
            "-I", str(ROOT / "include"), "-I", str(ROOT / "oracle"),
            "-L", str(PKG), "-lf3s_host", "-lf3s_hip",

@@ -38,6 +38,7 @@ hipError_t warm_runtime(hipStream_t s);
 hipError_t warm_convert(hipStream_t s);
 hipError_t warm_attention(hipStream_t s);
 hipError_t warm_bsf_util(hipStream_t s);
+hipError_t warm_naive(hipStream_t s);
 
 // Small grow-only device buffer (per call site).
 struct DeviceBuffer {

@@ -191,6 +191,7 @@ f3s_status f3s_init(void)
     F3S_HIP(warm_convert(nullptr));
     F3S_HIP(warm_attention(nullptr));
     F3S_HIP(warm_bsf_util(nullptr));
+    F3S_HIP(warm_naive(nullptr));
     F3S_HIP(hipDeviceSynchronize());
     return F3S_OK;
 }

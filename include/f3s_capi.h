@@ -121,6 +121,15 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
                              const int32_t* d_window_order, int32_t W, int32_t n,
                              int32_t d, int32_t H, float scale, void* stream);
 
+/* f3s_naive_baseline_kernel (baselines/gpu_baseline.cu:28-116): the naive
+ * edge-exact comparator, one thread per node, fp32 Q/K/V/O [n][d], CSR
+ * neighbours as stored (a duplicate entry counts twice, as in
+ * cpu_sparse_attention_csr).  No device-heap allocation (the reference
+ * mallocs per thread).  1 <= d <= 64. */
+f3s_status f3s_naive_attention_fwd(const float* Q, const float* K, const float* V, float* O,
+                                   const int32_t* d_row_ptr, const int32_t* d_col_idx,
+                                   int32_t n, int32_t d, float scale, void* stream);
+
 /* Planned execution (no reference counterpart; the reference relies on the
  * window sort alone, include/utils.cuh:48-59).  A plan splits windows with
  * more than `seg_tiles` tiles (0 = automatic: none on small graphs) into

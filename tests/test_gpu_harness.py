@@ -27,6 +27,17 @@ def test_harness(gpu, args):
     assert "SUCCESS" in r.stdout and "bit-exact" in r.stdout
 
 
+@pytest.mark.parametrize("args", [[], [str(GOLDEN / "cora"), "--same-qkv"]])
+def test_baselines_harness(gpu, args):
+    exe = ROOT / "tests" / "cpp" / "bin" / "test_baselines"
+    assert exe.exists(), "harness binary missing: run __graft_entry__.build()"
+    r = subprocess.run([str(exe), *args], capture_output=True, text=True, timeout=120,
+                       cwd=str(ROOT))
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stderr
+    assert "SUCCESS" in r.stdout
+
+
 def test_smoke_entry(gpu):
     import __graft_entry__ as ge
     ge.smoke()

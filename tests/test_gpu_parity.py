@@ -329,6 +329,35 @@ def test_attention_rejects_bad_args(gpu):
     assert e.value.name == "F3S_EUNSUPPORTED"
 
 
+# ------------------------------------------------------ naive comparator
+
+@pytest.mark.parametrize("case", ["cora", "random", "multigraph"])
+def test_naive_comparator(gpu, case):
+    """The naive edge-exact GPU comparator (baselines/gpu_baseline.cu) against
+    the oracle at the reference's 1e-4 (tests/test_baselines.cu:27),
+    including zero-degree rows and duplicate CSR entries (counted twice)."""
+    if case == "cora":
+        g = gpu.load_csr_graph(str(GOLDEN / "cora"))
+        rp, ci = g.row_ptr, g.col_ind
+    elif case == "random":
+        rp, ci = random_csr(700, 9, 3, self_loops=False)
+    else:
+        rp = np.array([0, 3, 3, 5, 9], np.int32)
+        ci = np.array([1, 1, 2, 0, 0, 3, 3, 3, 1], np.int32)
+    n, d = len(rp) - 1, 64
+    r = rng(7)
+    Q, K, V = (r.uniform(-1, 1, (n, d)).astype(np.float32) for _ in range(3))
+    csr = gpu.DeviceCSR(rp, ci)
+    dQ, dK, dV = (gpu.DeviceArray.from_numpy(x) for x in (Q, K, V))
+    dO = gpu.DeviceArray((n, d), np.float32)
+    dO.fill_bytes(0xFF)
+    gpu.naive_attention_fwd(dQ, dK, dV, dO, csr, d=d)
+    gpu.synchronize()
+    want = orc.masked_attention(n, d, 1, Q, K, V, rp, ci)[:, 0]
+    got = dO.numpy()
+    assert np.max(np.abs(got - want)) <= 1e-4
+
+
 # ------------------------------------------------- full-size configurations
 
 def sample_rows(bsf_host, n, extra_windows=8, stride_rows=4000, seed=0):
