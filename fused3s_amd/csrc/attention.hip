@@ -259,10 +259,21 @@ __device__ __forceinline__ void chunk_step(RowState& st, const h8 (&ka)[2], cons
 // in memory ([n][H][d]), which measured faster on config 5 than visiting the
 // heads one after another (smaller per-head L2 working set, but scattered
 // 128-byte fetches).  The register budget is capped for 4 waves per SIMD.
-template <int H, bool MASKED, int WPG>
+enum Mode : int {
+    kModeRing = 0,    // masked, tiles expanded on every pass (unplanned launch)
+    kModeList = 1,    // masked, compiled column lists (planned + compiled)
+    kModeDense = 2,   // tile-dense semantics
+};
+
+// The pass is bound by memory throughput, not latency: keeping a second
+// chunk's gathers in flight per wave (double-buffered registers, 3 waves per
+// SIMD) measured no faster than one chunk per wave at 4-5 waves per SIMD, so
+// the simpler single-buffered loop is kept.
+template <int H, int MODE, int WPG>
 __global__ void __launch_bounds__(kWave * WPG) __attribute__((amdgpu_waves_per_eu(4)))
 fused_attention_kernel(const AttnParams p)
 {
+    constexpr bool MASKED = MODE != kModeDense;
     __shared__ WaveLds lds_all[WPG];
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
@@ -312,8 +323,8 @@ fused_attention_kernel(const AttnParams p)
 #pragma unroll
     for (int t = 0; t < 4; ++t) st.acc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
-    if constexpr (MASKED) {
-      if (p.chunk_base) {
+    if constexpr (MODE == kModeList) {
+      {
         // ---- compiled plan: the attended columns were listed once per graph ----
         const int rbit = (r & 1) ? 16 + (r >> 1) : (r >> 1);
         const int64_t cb = p.chunk_base[item_idx], ce = p.chunk_base[item_idx + 1];
@@ -349,7 +360,9 @@ fused_attention_kernel(const AttnParams p)
                 (((rb.z >> rbit) & 1u) << 6) | (((rb.w >> rbit) & 1u) << 7);
             chunk_step(st, ka, kb, q0, q1, valid, vrow, L.v, lane, p.scale_log2);
         }
-      } else {
+      }
+    } else if constexpr (MODE == kModeRing) {
+      {
         // ---- column-compacted path: a ring of attended columns ----
         const uint16_t* __restrict__ tile_mask = p.tile_mask;
         const int rbit = (r & 1) ? 16 + (r >> 1) : (r >> 1);   // row r in a ring row mask
@@ -708,15 +721,15 @@ static f3s_status check_attention_args(const void* Q, const void* K, const void*
     return F3S_OK;
 }
 
-template <int H, bool MASKED>
+template <int H, int MODE>
 static void launch_hm(const AttnParams& p, int64_t waves, hipStream_t st)
 {
     // Small launches use one-wave workgroups so they spread over all CUs.
     if (waves < 4 * 256 * 2) {
-        hipLaunchKernelGGL((fused_attention_kernel<H, MASKED, 1>), dim3((unsigned)waves),
+        hipLaunchKernelGGL((fused_attention_kernel<H, MODE, 1>), dim3((unsigned)waves),
                            dim3(kWave), 0, st, p);
     } else {
-        hipLaunchKernelGGL((fused_attention_kernel<H, MASKED, 4>),
+        hipLaunchKernelGGL((fused_attention_kernel<H, MODE, 4>),
                            dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
     }
     if (p.num_split > 0)
@@ -727,10 +740,12 @@ static void launch_hm(const AttnParams& p, int64_t waves, hipStream_t st)
 template <int H>
 static void launch_h(const AttnParams& p, int64_t waves, hipStream_t st)
 {
-    if (p.tile_mask)
-        launch_hm<H, true>(p, waves, st);
+    if (!p.tile_mask)
+        launch_hm<H, kModeDense>(p, waves, st);
+    else if (p.chunk_base)
+        launch_hm<H, kModeList>(p, waves, st);
     else
-        launch_hm<H, false>(p, waves, st);
+        launch_hm<H, kModeRing>(p, waves, st);
 }
 
 static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
