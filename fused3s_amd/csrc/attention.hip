@@ -73,10 +73,14 @@ struct SplitInfo {
     int32_t w, first_slot, nseg, pad;
 };
 
+// Staging rows of 144 bytes: the 16 lanes that read one 16-byte piece of
+// 16 consecutive rows then hit 64 distinct LDS banks.
+constexpr int kStageRow = kD + 8;   // halves
+
 struct __align__(16) WaveLds {
     uint32_t off[kRing];   // byte offset of the slot's K/V row for this wave's head
     uint32_t rm[kRing];    // rows of the window that attend the slot
-    _Float16 v[kChunk * kD];
+    _Float16 stage[kChunk * kStageRow];   // the chunk's K rows, then its V rows
 };
 
 struct AttnParams {
@@ -190,18 +194,33 @@ constexpr float kLazy = 8.0f;
 // One chunk of 32 attended columns for the wave: S^T = K.Q^T, the masked
 // online-softmax update of row r, and O^T += V^T.P^T.  `valid` bit j says
 // whether the lane's j-th logit (slot slot_of(g, j)) is attended by row r.
-// vrow[i] holds 16 bytes of the V row of slot (lane >> 3) + 8i.
-__device__ __forceinline__ void chunk_step(RowState& st, const h8 (&ka)[2], const h8 (&kb)[2],
+// krow[i] / vrow[i] hold 16 bytes (piece lane & 7) of the K / V row of slot
+// (lane >> 3) + 8i: gathered in this layout, eight consecutive lanes read one
+// 128-byte row, which the vector-memory address unit coalesces; the LDS
+// stage then hands K out in MFMA A-operand layout (lane (g, r): slots r and
+// 16 + r, dims 8g.. and 32 + 8g..) and V transposed.
+__device__ __forceinline__ void chunk_step(RowState& st, const h8 (&krow)[4],
                                            const h8 q0, const h8 q1, uint32_t valid,
-                                           const h8 (&vrow)[4], _Float16* __restrict__ vl,
+                                           const h8 (&vrow)[4], _Float16* __restrict__ stage,
                                            int lane, float scale_log2)
 {
     const int g = lane >> 4, r = lane & 15;
+    F3S_WAVE_LDS_SYNC();   // previous chunk's V reads are complete
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int s = (lane >> 3) + 8 * i;
+        *reinterpret_cast<h8*>(&stage[s * kStageRow + 8 * (lane & 7)]) = krow[i];
+    }
+    F3S_WAVE_LDS_SYNC();
+    const h8 ka0 = *reinterpret_cast<const h8*>(&stage[r * kStageRow + 8 * g]);
+    const h8 ka1 = *reinterpret_cast<const h8*>(&stage[r * kStageRow + 32 + 8 * g]);
+    const h8 kb0 = *reinterpret_cast<const h8*>(&stage[(16 + r) * kStageRow + 8 * g]);
+    const h8 kb1 = *reinterpret_cast<const h8*>(&stage[(16 + r) * kStageRow + 32 + 8 * g]);
     f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-    s0 = mfma16x16x32(ka[0], q0, s0);
-    s0 = mfma16x16x32(ka[1], q1, s0);
-    s1 = mfma16x16x32(kb[0], q0, s1);
-    s1 = mfma16x16x32(kb[1], q1, s1);
+    s0 = mfma16x16x32(ka0, q0, s0);
+    s0 = mfma16x16x32(ka1, q1, s0);
+    s1 = mfma16x16x32(kb0, q0, s1);
+    s1 = mfma16x16x32(kb1, q1, s1);
 
     float x[8];
 #pragma unroll
@@ -233,18 +252,18 @@ __device__ __forceinline__ void chunk_step(RowState& st, const h8 (&ka)[2], cons
     st.l = __builtin_amdgcn_fdot2(h2{pb[4], pb[5]}, ones, st.l, false);
     st.l = __builtin_amdgcn_fdot2(h2{pb[6], pb[7]}, ones, st.l, false);
 
-    // V through LDS, transposed into A operands
-    F3S_WAVE_LDS_SYNC();   // previous chunk's V reads are complete
+    // V through the same stage, transposed into A operands
+    F3S_WAVE_LDS_SYNC();   // K reads are complete
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int s = (lane >> 3) + 8 * i;
-        *reinterpret_cast<h8*>(&vl[s * kD + 8 * (lane & 7)]) = vrow[i];
+        *reinterpret_cast<h8*>(&stage[s * kStageRow + 8 * (lane & 7)]) = vrow[i];
     }
     F3S_WAVE_LDS_SYNC();
     h8 va[4];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const h4 q = *reinterpret_cast<const h4*>(&vl[slot_of(g, j) * kD + 4 * r]);
+        const h4 q = *reinterpret_cast<const h4*>(&stage[slot_of(g, j) * kStageRow + 4 * r]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) va[t][j] = q[t];
     }
@@ -326,39 +345,35 @@ fused_attention_kernel(const AttnParams p)
     if constexpr (MODE == kModeList) {
       {
         // ---- compiled plan: the attended columns were listed once per graph ----
+        // The chunk's 256-byte record (32 offsets, 32 row masks) is read with
+        // one coalesced load, lane l <- word l, one chunk ahead, and handed
+        // out through LDS: the vector-memory address path, not HBM, bounds
+        // this pass, so it gets one instruction instead of eight.
         const int rbit = (r & 1) ? 16 + (r >> 1) : (r >> 1);
         const int64_t cb = p.chunk_base[item_idx], ce = p.chunk_base[item_idx + 1];
-        const uint32_t add = head_off + 16 * g;
-        uint32_t mk0 = 0, mk1 = 0, mv[4] = {0, 0, 0, 0};
-        uint4 mra = make_uint4(0, 0, 0, 0), mrb = make_uint4(0, 0, 0, 0);
-        auto load_meta = [&](int64_t c) {
-            const uint32_t* rec = p.columns + c * 64;
-            mk0 = rec[r];
-            mk1 = rec[16 + r];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mv[i] = rec[(lane >> 3) + 8 * i];
-            mra = *reinterpret_cast<const uint4*>(rec + 32 + 4 * g);
-            mrb = *reinterpret_cast<const uint4*>(rec + 48 + 4 * g);
-        };
-        if (cb < ce) load_meta(cb);
+        const uint32_t piece_off = head_off + 16 * (lane & 7);
+        uint32_t* meta = reinterpret_cast<uint32_t*>(L.off);   // 64 words of this wave's ring
+        uint32_t word = cb < ce ? p.columns[cb * 64 + lane] : 0u;
         for (int64_t c = cb; c < ce; ++c) {
-            const uint32_t o0 = mk0 + add, o1 = mk1 + add;
-            uint32_t vo[4];
+            F3S_WAVE_LDS_SYNC();   // the previous chunk's reads of meta are done
+            meta[lane] = word;
+            F3S_WAVE_LDS_SYNC();
+            if (c + 1 < ce) word = p.columns[(c + 1) * 64 + lane];   // next record, in flight
+            h8 krow[4], vrow[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) vo[i] = mv[i] + head_off + 16 * (lane & 7);
-            const uint4 ra = mra, rb = mrb;
-            if (c + 1 < ce) load_meta(c + 1);   // next chunk's list, while this one runs
-            const h8 ka[2] = {load_h8(kres, o0), load_h8(kres, o0 + 64)};
-            const h8 kb[2] = {load_h8(kres, o1), load_h8(kres, o1 + 64)};
-            h8 vrow[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) vrow[i] = load_h8(vres, vo[i]);
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t o = meta[(lane >> 3) + 8 * i] + piece_off;
+                krow[i] = load_h8(kres, o);
+                vrow[i] = load_h8(vres, o);
+            }
+            const uint4 ra = *reinterpret_cast<const uint4*>(&meta[32 + 4 * g]);
+            const uint4 rb = *reinterpret_cast<const uint4*>(&meta[48 + 4 * g]);
             const uint32_t valid =
                 ((ra.x >> rbit) & 1u) | (((ra.y >> rbit) & 1u) << 1) |
                 (((ra.z >> rbit) & 1u) << 2) | (((ra.w >> rbit) & 1u) << 3) |
                 (((rb.x >> rbit) & 1u) << 4) | (((rb.y >> rbit) & 1u) << 5) |
                 (((rb.z >> rbit) & 1u) << 6) | (((rb.w >> rbit) & 1u) << 7);
-            chunk_step(st, ka, kb, q0, q1, valid, vrow, L.v, lane, p.scale_log2);
+            chunk_step(st, krow, q0, q1, valid, vrow, L.stage, lane, p.scale_log2);
         }
       }
     } else if constexpr (MODE == kModeRing) {
@@ -423,13 +438,13 @@ fused_attention_kernel(const AttnParams p)
             // so a chunk never wraps around the ring.
             const uint32_t* off = &L.off[head & kMask];
             const uint32_t* rmr = &L.rm[head & kMask];
-            const uint32_t o0 = off[r] + 16 * g, o1 = off[16 + r] + 16 * g;
-            const h8 ka[2] = {load_h8(kres, o0), load_h8(kres, o0 + 64)};
-            const h8 kb[2] = {load_h8(kres, o1), load_h8(kres, o1 + 64)};
-            h8 vrow[4];
+            h8 krow[4], vrow[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                vrow[i] = load_h8(vres, off[(lane >> 3) + 8 * i] + 16 * (lane & 7));
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t o = off[(lane >> 3) + 8 * i] + 16 * (lane & 7);
+                krow[i] = load_h8(kres, o);
+                vrow[i] = load_h8(vres, o);
+            }
             const uint4 ra = *reinterpret_cast<const uint4*>(&rmr[4 * g]);
             const uint4 rb = *reinterpret_cast<const uint4*>(&rmr[16 + 4 * g]);
             const uint32_t valid =
@@ -437,7 +452,7 @@ fused_attention_kernel(const AttnParams p)
                 (((ra.z >> rbit) & 1u) << 2) | (((ra.w >> rbit) & 1u) << 3) |
                 (((rb.x >> rbit) & 1u) << 4) | (((rb.y >> rbit) & 1u) << 5) |
                 (((rb.z >> rbit) & 1u) << 6) | (((rb.w >> rbit) & 1u) << 7);
-            chunk_step(st, ka, kb, q0, q1, valid, vrow, L.v, lane, p.scale_log2);
+            chunk_step(st, krow, q0, q1, valid, vrow, L.stage, lane, p.scale_log2);
             head += pending < kChunk ? pending : kChunk;
         }
       }
@@ -451,15 +466,14 @@ fused_attention_kernel(const AttnParams p)
             auto row_at = [&](bool ok, int32_t c, int s) -> uint32_t {
                 return ok && c + s < n ? (uint32_t)(c + s) * row_stride + head_off : kNoRow;
             };
-            const uint32_t o0 = row_at(ok0, c0, r) + 16 * g, o1 = row_at(ok1, c1, r) + 16 * g;
-            const h8 ka[2] = {load_h8(kres, o0), load_h8(kres, o0 + 64)};
-            const h8 kb[2] = {load_h8(kres, o1), load_h8(kres, o1 + 64)};
-            h8 vrow[4];
+            h8 krow[4], vrow[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int s = (lane >> 3) + 8 * i;   // slots 0-15: tile t, 16-31: tile t+1
-                const uint32_t vo = s < 16 ? row_at(ok0, c0, s) : row_at(ok1, c1, s - 16);
-                vrow[i] = load_h8(vres, vo + 16 * (lane & 7));
+                const uint32_t o = (s < 16 ? row_at(ok0, c0, s) : row_at(ok1, c1, s - 16)) +
+                                   16 * (lane & 7);
+                krow[i] = load_h8(kres, o);
+                vrow[i] = load_h8(vres, o);
             }
             // logit j of the lane is column 4g + j of tile t (j < 4) or
             // 4g + j - 4 of tile t+1; attended iff the column exists
@@ -469,7 +483,7 @@ fused_attention_kernel(const AttnParams p)
                 valid |= (uint32_t)(ok0 && c0 + 4 * g + v < n) << v;
                 valid |= (uint32_t)(ok1 && c1 + 4 * g + v < n) << (4 + v);
             }
-            chunk_step(st, ka, kb, q0, q1, valid, vrow, L.v, lane, p.scale_log2);
+            chunk_step(st, krow, q0, q1, valid, vrow, L.stage, lane, p.scale_log2);
         }
     }
 
