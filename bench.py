@@ -110,10 +110,18 @@ def main() -> int:
         src = f3s.DeviceArray(nb, np.uint8, zero=True)
         dst = f3s.DeviceArray(nb, np.uint8)
         from fused3s_amd import _lib
+        e0, e1 = f3s.Event(), f3s.Event()
+        times = []
         for _ in range(args.steps):
+            e0.record()
             _lib.hip().f3s_memcpy_d2d(dst.ptr, src.ptr, nb, None)
-        f3s.synchronize()
-        print(json.dumps({"copy_probe_bytes": nb, "launches": args.steps}), flush=True)
+            e1.record()
+            f3s.synchronize()
+            times.append(e0.elapsed_ms(e1))
+        best = min(times)
+        # read + write bytes over the fastest copy: the practical HBM rate
+        print(json.dumps({"copy_probe_bytes": nb, "launches": args.steps,
+                          "copy_ms": times, "copy_GBps_rw": 2 * nb / best / 1e6}), flush=True)
         return 0
     f3s.init()
     c = f3s.CONFIGS[args.config]

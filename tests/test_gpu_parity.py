@@ -180,9 +180,24 @@ def test_converter_hub_windows(gpu):
     check_converter(gpu, rp, ci)
 
 
+def test_converter_column_slices(gpu):
+    # more block columns than one LDS bitmap slice (131072): windows with edges
+    # in both slices, and a last slice whose word count is not a multiple of 4
+    n = 2_200_000
+    r = rng(11)
+    deg = r.integers(0, 4, n)
+    deg[:2000] += 3
+    rp = np.zeros(n + 1, np.int64)
+    rp[1:] = np.cumsum(deg)
+    ci = r.integers(0, n, int(rp[-1])).astype(np.int32)
+    ci[rp[:2000]] = n - 1 - r.integers(0, 40, 2000)   # far end of the last slice
+    ci[rp[:2000] + 1] = r.integers(0, 16 * 131072, 2000)
+    check_converter(gpu, rp.astype(np.int32), ci)
+
+
 def test_converter_unsorted_and_empty_windows(gpu):
     n = 64
-    rows = {0: [63, 1, 17], 5: [0], 48: [47, 3, 62, 16], 63: [63]}
+    rows = {0: [63, 1, 17, 1, 63], 5: [0, 0], 48: [47, 3, 62, 16], 63: [63]}
     rp = np.zeros(n + 1, np.int32)
     ci = []
     for u in range(n):
