@@ -38,6 +38,32 @@ def alg_bytes(n: int, W: int, T: int, occ_sum: int, H: int, d: int, masked: bool
             + occ_sum * H * d * 2 * 2)
 
 
+def convert_phases_ms(csr, bsf, stream) -> float:
+    """GPU time of f3s_convert_csr_to_bsf's count call plus its fill call into
+    the outputs of an earlier conversion of the same CSR (HIP events on the
+    launch stream around each call; the caller's allocation between the two
+    calls is left out)."""
+    import fused3s_amd as f3s
+    from fused3s_amd import _lib
+    from fused3s_amd.device import check
+    lib = _lib.hip()
+    e = [f3s.Event() for _ in range(4)]
+    T = C.c_int64(0)
+    e[0].record(stream)
+    check(lib.f3s_convert_csr_to_bsf(csr.row_ptr.ptr, csr.col_idx.ptr, csr.n, csr.nnz,
+                                     bsf.window_offsets.ptr, None, None, C.byref(T),
+                                     stream.handle), "convert(count)")
+    e[1].record(stream)
+    e[2].record(stream)
+    check(lib.f3s_convert_csr_to_bsf(csr.row_ptr.ptr, csr.col_idx.ptr, csr.n, csr.nnz,
+                                     bsf.window_offsets.ptr, bsf.block_col.ptr,
+                                     bsf.tile_mask.ptr, C.byref(T), stream.handle),
+          "convert(fill)")
+    e[3].record(stream)
+    f3s.synchronize()
+    return e[0].elapsed_ms(e[1]) + e[2].elapsed_ms(e[3])
+
+
 def read_traffic(kernel_prefix: str) -> float | None:
     """HBM bytes per launch from the committed rocprofv3 --pmc summary
     (profiles/pmc_traffic_cfg4.txt: 'bytes_per_launch <value>'), if any."""
@@ -137,12 +163,16 @@ def main() -> int:
     stream = f3s.Stream()
     csr = f3s.DeviceCSR(rp, ci, stream)
     ev0, ev1 = f3s.Event(), f3s.Event()
-    # converter (timed separately; not part of a step)
+    # converter (timed separately; not part of a step): end to end through
+    # the Python wrapper (output allocation included), and the two C-ABI
+    # phases alone into the already allocated outputs
     bsf = f3s.convert_device(csr, masks=True, stream=stream)
-    ev0.record(stream)
+    f3s.synchronize()
+    t_conv = time.perf_counter()
     bsf = f3s.convert_device(csr, masks=True, stream=stream)
-    ev1.record(stream)
-    conv_ms = ev0.elapsed_ms(ev1)
+    f3s.synchronize()
+    conv_e2e_ms = (time.perf_counter() - t_conv) * 1e3
+    conv_ms = convert_phases_ms(csr, bsf, stream)
     use_sorted = args.order == "sorted" or (args.order == "auto" and c.kind != "sbm")
     order = f3s.window_order_device(bsf, stream) if use_sorted else None
     ev0.record(stream)
@@ -214,6 +244,7 @@ def main() -> int:
         "alg_bytes_per_launch": nbytes,
         "mfma_frac_tile_model": flops_tile / (kavg * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
         "converter_us": conv_ms * 1e3,
+        "converter_end_to_end_us": conv_e2e_ms * 1e3,
         "plan_us": plan_ms * 1e3,
         "plan_compiled": bool(masked and not args.no_compile),
         "device": f3s.device_name(),

@@ -11,7 +11,7 @@ from .device import (DeviceArray, Event, F3SError, Stream, device_count, device_
                      synchronize)
 from .graph import (BlockSparseFormat, DeviceBSF, DeviceCSR, GraphData, bsf_stats,
                     convert_csr_to_block_sparse, convert_device, generate_balanced_window_order,
-                    load_csr_graph, window_order_device)
+                    load_csr_graph, load_graph, save_graph, window_order_device)
 from .attention import Plan, attention_fwd, cast_f32_to_f16, naive_attention_fwd
 from .configs import CONFIGS, Config
 
@@ -20,7 +20,7 @@ __all__ = [
     "synchronize",
     "BlockSparseFormat", "DeviceBSF", "DeviceCSR", "GraphData", "bsf_stats",
     "convert_csr_to_block_sparse", "convert_device", "generate_balanced_window_order",
-    "load_csr_graph", "window_order_device", "Plan", "attention_fwd", "cast_f32_to_f16",
-    "naive_attention_fwd",
+    "load_csr_graph", "load_graph", "save_graph", "window_order_device", "Plan",
+    "attention_fwd", "cast_f32_to_f16", "naive_attention_fwd",
     "CONFIGS", "Config",
 ]

@@ -69,6 +69,11 @@ HOST_API = {
                             C.POINTER(P_i32), C.POINTER(P_i32), P_i64]),
     "f3s_gen_features_f16": (c_i32, [c_u64, c_i32, c_i64, c_i32, c_vp]),
     "f3s_host_f16_to_f32": (None, [c_vp, c_vp, c_i64]),
+    "f3s_host_save_graph": (c_i32, [C.c_char_p, c_i32, c_i64, c_vp, c_vp, c_i32, c_i64,
+                                    c_vp, c_vp, c_vp]),
+    "f3s_host_load_graph": (c_i32, [C.c_char_p, P_i32, P_i64, C.POINTER(P_i32),
+                                    C.POINTER(P_i32), P_i32, P_i64, C.POINTER(P_i32),
+                                    C.POINTER(P_i32), C.POINTER(C.POINTER(C.c_uint16))]),
 }
 
 

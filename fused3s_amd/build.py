@@ -24,7 +24,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 HIP_SOURCES = ["runtime.hip", "convert.hip", "attention.hip", "bsf_util.hip", "naive.hip"]
-HOST_SOURCES = ["host/gen.cpp", "host/graph.cpp"]
+HOST_SOURCES = ["host/gen.cpp", "host/graph.cpp", "host/graph_file.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [

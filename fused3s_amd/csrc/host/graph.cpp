@@ -99,6 +99,46 @@ using namespace f3s_host;
 
 GraphData load_csr_graph(const std::string& dataset_dir) { return load(dataset_dir); }
 
+void save_graph_binary(const std::string& path, const GraphData& g, const blockSparseFormat* bsf)
+{
+    const bool has = bsf && !bsf->window_offsets.empty();
+    const bool masks = has && !bsf->block_col_indices.empty() &&
+                       bsf->tile_masks.size() == 16 * bsf->block_col_indices.size();
+    if (f3s_host_save_graph(path.c_str(), g.num_nodes, (int64_t)g.col_ind.size(),
+                            g.row_ptr.data(), g.col_ind.data(), has ? bsf->num_row_windows : 0,
+                            has ? (int64_t)bsf->block_col_indices.size() : 0,
+                            has ? bsf->window_offsets.data() : nullptr,
+                            has ? bsf->block_col_indices.data() : nullptr,
+                            masks ? bsf->tile_masks.data() : nullptr) != 0)
+        throw std::runtime_error(f3s_host_last_error());
+}
+
+GraphData load_graph_binary(const std::string& path, blockSparseFormat* bsf)
+{
+    int32_t n = 0, W = 0;
+    int64_t nnz = 0, T = 0;
+    int32_t *rp = nullptr, *ci = nullptr, *wo = nullptr, *bc = nullptr;
+    uint16_t* tm = nullptr;
+    if (f3s_host_load_graph(path.c_str(), &n, &nnz, &rp, &ci, &W, &T, &wo, &bc, &tm) != 0)
+        throw std::runtime_error(f3s_host_last_error());
+    GraphData g;
+    g.num_nodes = n;
+    g.num_edges = (int)nnz;
+    g.row_ptr.assign(rp, rp + n + 1);
+    g.col_ind.assign(ci, ci + nnz);
+    if (bsf) {
+        *bsf = blockSparseFormat{};
+        if (wo) {
+            bsf->num_row_windows = W;
+            bsf->window_offsets.assign(wo, wo + W + 1);
+            bsf->block_col_indices.assign(bc, bc + T);
+            if (tm) bsf->tile_masks.assign(tm, tm + 16 * T);
+        }
+    }
+    for (void* p : {(void*)rp, (void*)ci, (void*)wo, (void*)bc, (void*)tm}) free(p);
+    return g;
+}
+
 blockSparseFormat convert_csr_to_block_sparse(int num_nodes, const std::vector<int>& row_ptr,
                                               const std::vector<int>& col_ind)
 {

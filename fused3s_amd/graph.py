@@ -57,6 +57,53 @@ def load_csr_graph(dataset_dir: str) -> GraphData:
     return GraphData(int(n.value), int(nnz.value), _take_i32(rp, n.value + 1), _take_i32(ci, nnz.value))
 
 
+def save_graph(path: str, row_ptr, col_ind, bsf: BlockSparseFormat | None = None) -> None:
+    """Writes the CSR (and the block-sparse form, with its row masks when it
+    holds them) to one checksummed binary file (f3s_host_save_graph)."""
+    rp = np.ascontiguousarray(row_ptr, np.int32)
+    ci = np.ascontiguousarray(col_ind, np.int32)
+    n = len(rp) - 1
+    args = [None, None, None]
+    W, T = 0, 0
+    if bsf is not None:
+        wo = np.ascontiguousarray(bsf.window_offsets, np.int32)
+        bc = np.ascontiguousarray(bsf.block_col_indices, np.int32)
+        W, T = int(bsf.num_row_windows), len(bc)
+        tm = (np.ascontiguousarray(bsf.tile_masks, np.uint16)
+              if len(bsf.tile_masks) == T and T > 0 else None)
+        args = [wo.ctypes.data, bc.ctypes.data, tm.ctypes.data if tm is not None else None]
+    lib = _lib.host()
+    if lib.f3s_host_save_graph(os.fsencode(path), n, len(ci), rp.ctypes.data, ci.ctypes.data,
+                               W, T, *args) != 0:
+        raise RuntimeError(lib.f3s_host_last_error().decode())
+
+
+def load_graph(path: str) -> tuple[GraphData, BlockSparseFormat | None]:
+    """Reads a file written by save_graph (f3s_host_load_graph); raises
+    RuntimeError on any corruption or invariant violation."""
+    n, nnz, W, T = C.c_int32(), C.c_int64(), C.c_int32(), C.c_int64()
+    rp, ci, wo, bc = (C.POINTER(C.c_int32)() for _ in range(4))
+    tm = C.POINTER(C.c_uint16)()
+    lib = _lib.host()
+    if lib.f3s_host_load_graph(os.fsencode(path), C.byref(n), C.byref(nnz), C.byref(rp),
+                               C.byref(ci), C.byref(W), C.byref(T), C.byref(wo), C.byref(bc),
+                               C.byref(tm)) != 0:
+        raise RuntimeError(lib.f3s_host_last_error().decode())
+    g = GraphData(int(n.value), int(nnz.value), _take_i32(rp, n.value + 1),
+                  _take_i32(ci, nnz.value))
+    if not wo:
+        return g, None
+    masks = np.zeros((0, 16), np.uint16)
+    if tm:
+        try:
+            if T.value:
+                masks = np.ctypeslib.as_array(tm, shape=(T.value * 16,)).copy().reshape(-1, 16)
+        finally:
+            lib.f3s_host_free(C.cast(tm, C.c_void_p))
+    return g, BlockSparseFormat(int(W.value), _take_i32(wo, W.value + 1),
+                                _take_i32(bc, T.value), masks)
+
+
 class DeviceCSR:
     """A CSR graph resident in device memory."""
 

@@ -58,3 +58,12 @@ blockSparseFormat convert_csr_to_block_sparse(int num_nodes, const std::vector<i
 
 // include/utils.cuh:48-59
 std::vector<int> generate_balanced_window_order(const blockSparseFormat& format);
+
+// Binary graph file (f3s_host_save_graph / f3s_host_load_graph; no
+// counterpart in the reference, which reads text only): the CSR and,
+// optionally, its block-sparse form with row masks.  Both throw
+// std::runtime_error on failure; load fills *bsf when it is not NULL and the
+// file holds a block-sparse section (else leaves it empty).
+void save_graph_binary(const std::string& path, const GraphData& graph,
+                       const blockSparseFormat* bsf = nullptr);
+GraphData load_graph_binary(const std::string& path, blockSparseFormat* bsf = nullptr);

@@ -31,6 +31,23 @@ const char* f3s_host_last_error(void);
 int32_t f3s_host_load_csr(const char* dir, int32_t* n, int64_t* nnz, int32_t** row_ptr,
                           int32_t** col_idx);
 
+/* Binary graph file (no counterpart in the reference, which keeps only the
+ * text files read by load_csr_graph, include/utils.cuh:26-40): the CSR and,
+ * when window_offsets is given, its block-sparse form (W = ceil(n/16) windows,
+ * T tiles, and the 16 row masks per tile when tile_mask is given), in one
+ * checksummed file with 64-byte-aligned arrays.  The file is written to
+ * <path>.tmp and renamed, so a reader never sees a partial file.
+ * f3s_host_load_graph validates header, size, checksum, CSR and block-sparse
+ * invariants and returns library-allocated arrays (window_offsets,
+ * block_col and tile_mask are NULL, W and T 0, when the file has none). */
+int32_t f3s_host_save_graph(const char* path, int32_t n, int64_t nnz, const int32_t* row_ptr,
+                            const int32_t* col_idx, int32_t W, int64_t T,
+                            const int32_t* window_offsets, const int32_t* block_col,
+                            const uint16_t* tile_mask);
+int32_t f3s_host_load_graph(const char* path, int32_t* n, int64_t* nnz, int32_t** row_ptr,
+                            int32_t** col_idx, int32_t* W, int64_t* T, int32_t** window_offsets,
+                            int32_t** block_col, uint16_t** tile_mask);
+
 /* generate_balanced_window_order (include/utils.cuh:48-59): std::sort of
  * iota(W) by descending tile count with the reference's comparator. */
 int32_t f3s_host_window_order(const int32_t* window_offsets, int32_t W, int32_t* order);

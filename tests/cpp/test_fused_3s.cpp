@@ -15,6 +15,9 @@
 //                 [--zero-columns]  (every column index read as 0: the graph the
 //                 reference's as-shipped loader produces, include/utils.cuh:36,
 //                 on which its published kernel times were measured)
+//                 [--save-graph FILE]  (write the graph and its block-sparse form
+//                 to a binary graph file; a dataset path ending in .f3sg is read
+//                 as such a file instead of a text directory)
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -76,12 +79,14 @@ int main(int argc, char** argv)
     bool masked = true;
     int reps = 20, cfg = 0;
     bool zero_columns = false;
+    std::string save_path;
     for (int i = 1; i < argc; ++i) {
         std::string a = argv[i];
         if (a == "--semantics" && i + 1 < argc) masked = std::string(argv[++i]) != "tile_dense";
         else if (a == "--reps" && i + 1 < argc) reps = atoi(argv[++i]);
         else if (a == "--config" && i + 1 < argc) cfg = atoi(argv[++i]);
         else if (a == "--zero-columns") zero_columns = true;
+        else if (a == "--save-graph" && i + 1 < argc) save_path = argv[++i];
         else dataset_path = a;
     }
     const int feat_dim = 64;
@@ -101,7 +106,11 @@ int main(int argc, char** argv)
             graph = synthetic(cfg);
         } else {
             std::cout << "Loading graph from: " << dataset_path << std::endl;
-            graph = load_csr_graph(dataset_path);
+            const std::string ext = ".f3sg";
+            const bool binary = dataset_path.size() > ext.size() &&
+                                dataset_path.compare(dataset_path.size() - ext.size(),
+                                                     ext.size(), ext) == 0;
+            graph = binary ? load_graph_binary(dataset_path) : load_csr_graph(dataset_path);
         }
     } catch (const std::exception& e) {
         std::cerr << "FAILURE: " << e.what() << std::endl;
@@ -111,6 +120,15 @@ int main(int argc, char** argv)
     const int n = graph.num_nodes;
     blockSparseFormat format = convert_csr_to_block_sparse(n, graph.row_ptr, graph.col_ind);
     std::vector<int> window_order = generate_balanced_window_order(format);
+    if (!save_path.empty()) {
+        try {
+            save_graph_binary(save_path, graph, &format);
+            std::cout << "Saved graph file: " << save_path << std::endl;
+        } catch (const std::exception& e) {
+            std::cerr << "FAILURE: " << e.what() << std::endl;
+            return 1;
+        }
+    }
     const int W = format.num_row_windows;
     const int64_t T = (int64_t)format.block_col_indices.size();
 

@@ -27,6 +27,25 @@ def test_harness(gpu, args):
     assert "SUCCESS" in r.stdout and "bit-exact" in r.stdout
 
 
+def test_harness_binary_graph_file(gpu, tmp_path):
+    # text dataset -> binary graph file (with the GPU converter's block-sparse
+    # form) -> the harness again, reading the binary file
+    path = tmp_path / "citeseer.f3sg"
+    for args in ([str(GOLDEN / "citeseer"), "--save-graph", str(path)], [str(path)]):
+        r = subprocess.run([str(EXE), *args, "--reps", "3"], capture_output=True, text=True,
+                           timeout=120)
+        print(r.stdout[-1500:], r.stderr[-1500:], flush=True)
+        assert r.returncode == 0, r.stderr
+        assert "SUCCESS" in r.stdout and "bit-exact" in r.stdout
+    import fused3s_amd as f3s
+    g, bsf = f3s.load_graph(str(path))
+    ref = f3s.convert_device(f3s.DeviceCSR(g.row_ptr, g.col_ind)).to_host()
+    assert bsf is not None and len(bsf.block_col_indices) == 7467
+    assert (bsf.window_offsets == ref.window_offsets).all()
+    assert (bsf.block_col_indices == ref.block_col_indices).all()
+    assert (bsf.tile_masks == ref.tile_masks).all()
+
+
 @pytest.mark.parametrize("args", [[], [str(GOLDEN / "cora"), "--same-qkv"]])
 def test_baselines_harness(gpu, args):
     exe = ROOT / "tests" / "cpp" / "bin" / "test_baselines"
