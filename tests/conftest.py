@@ -11,6 +11,15 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+# torch bundles its own HIP runtime; libf3s_hip.so binds to whichever
+# libamdhip64.so.7 the process loads first.  Importing torch before any test
+# touches the library keeps one runtime in the test process, so the torch
+# binding's tests can share it with the rest of the suite.
+try:
+    import torch  # noqa: F401
+except ImportError:   # the library itself does not need torch
+    torch = None
+
 ROOT = Path(__file__).resolve().parents[1]
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))

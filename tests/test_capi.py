@@ -60,8 +60,10 @@ def test_validation_happens_before_device_access():
     assert h.f3s_cast_f32_to_f16(None, None, -1, None) == 1
 
 
-@pytest.mark.skipif(f3s.device_count() > 0, reason="checks the no-GPU behaviour")
 def test_no_device_is_reported_not_faked():
+    # decided at run time, not at collection: no HIP call while collecting
+    if f3s.device_count() > 0:
+        pytest.skip("checks the no-GPU behaviour")
     h = _lib.hip()
     p = C.c_void_p()
     assert h.f3s_malloc(C.byref(p), 16) == 4      # F3S_ENODEV
