@@ -64,11 +64,14 @@ def convert_phases_ms(csr, bsf, stream) -> float:
     return e[0].elapsed_ms(e[1]) + e[2].elapsed_ms(e[3])
 
 
-def read_traffic(kernel_prefix: str) -> float | None:
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary
-    (profiles/pmc_traffic_cfg4.txt: 'bytes_per_launch <value>'), if any."""
-    p = ROOT / "profiles" / "pmc_traffic_cfg4.txt"
-    if not p.exists():
+def read_traffic(cfg: int, default_pass: bool) -> float | None:
+    """HBM bytes per launch of the fused pass from the committed rocprofv3
+    --pmc summary of this configuration (profiles/pmc_traffic_cfg<N>.txt:
+    'bytes_per_launch <value>'); those were measured on the default pass
+    (masked, compiled plan, default order and segments), so other passes get
+    None."""
+    p = ROOT / "profiles" / f"pmc_traffic_cfg{cfg}.txt"
+    if not default_pass or not p.exists():
         return None
     for line in p.read_text().splitlines():
         parts = line.split()
@@ -217,7 +220,8 @@ def main() -> int:
     nbytes = alg_bytes(n, bsf.W, bsf.T, occ_sum, H, d, masked)
     achieved = nbytes / (kavg * 1e-3) / 1e9
     flops_tile = bsf.T * 4 * 16 * 16 * d * H
-    traffic = read_traffic("fused_attention_kernel")
+    traffic = read_traffic(c.cfg, masked and not args.no_compile and args.order == "auto"
+                           and args.seg == 0)
     res = {
         "metric": "fused attention edges/s + kernel us; achieved HBM GB/s (% of peak) on 1 MI355X",
         "value": nnz * args.steps / wall,
