@@ -63,7 +63,6 @@ constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-rob
 // 32-bit data format, no swizzle.  Offsets >= num_records read as 0.
 constexpr int32_t kBufferFlags = 0x00020000;
 // Row-mask layout in the ring: bit k = row 2k, bit 16 + k = row 2k + 1.
-constexpr uint32_t kAllRows = 0x00ff00ffu;
 
 struct Item {
     int32_t w, tb, te, slot;       // slot < 0: whole window, write O directly
@@ -292,7 +291,6 @@ template <int H, int MODE, int WPG>
 __global__ void __launch_bounds__(kWave * WPG) __attribute__((amdgpu_waves_per_eu(4)))
 fused_attention_kernel(const AttnParams p)
 {
-    constexpr bool MASKED = MODE != kModeDense;
     __shared__ WaveLds lds_all[WPG];
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
@@ -698,11 +696,23 @@ plan_columns(const Item* __restrict__ items, int64_t num_items,
 
 }  // namespace f3s
 
-struct f3s_plan {
-    int32_t W = 0, H = 1, seg = 0;
-    int32_t natural_order = 1;   // no window order given: keep neighbours on one XCD
-    int64_t T = 0, num_items = 0, num_split = 0, num_slots = 0;
+// Work items of one segment size: windows with more than `seg` tiles are cut
+// into segments whose (m, l, O) partials a second launch merges.
+struct f3s_item_set {
+    int32_t seg = 0;
+    int64_t num_items = 0, num_split = 0, num_slots = 0;
     f3s::DeviceBuffer items, splits, partials;
+};
+
+struct f3s_plan {
+    int32_t W = 0, H = 1;
+    int32_t natural_order = 1;   // no window order given: keep neighbours on one XCD
+    int64_t T = 0;
+    // Masked passes (compiled lists or tile expansion) run `masked`.  A
+    // tile-dense chunk costs two whole tiles, about 15x a masked chunk per
+    // tile on sparse graphs, so tile-dense passes run `dense`, cut finer;
+    // dense.seg == 0 means they share `masked` (an explicit segment size).
+    f3s_item_set masked, dense;
     // compiled column lists (f3s_plan_compile) and the structure they describe
     f3s::DeviceBuffer chunk_base, columns;
     const int32_t* compiled_block_col = nullptr;
@@ -712,6 +722,60 @@ struct f3s_plan {
 };
 
 namespace f3s {
+
+static f3s_status build_items(f3s_item_set& set, const int32_t* d_window_offsets,
+                              const int32_t* d_window_order, int32_t W, int32_t H, int64_t seg,
+                              hipStream_t st)
+{
+    if (seg > INT32_MAX) seg = INT32_MAX;
+    set.seg = (int32_t)seg;
+    DeviceBuffer cnt_items, cnt_slots, cnt_split, base_items, base_slots, base_split, tmp;
+    f3s_status s;
+    if ((s = cnt_items.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
+        (s = cnt_slots.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
+        (s = cnt_split.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
+        (s = base_items.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
+        (s = base_slots.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
+        (s = base_split.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
+        (s = tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(W))) != F3S_OK)
+        return s;
+    auto* ci = reinterpret_cast<int32_t*>(cnt_items.ptr);
+    auto* cs = reinterpret_cast<int32_t*>(cnt_slots.ptr);
+    auto* cp = reinterpret_cast<int32_t*>(cnt_split.ptr);
+    auto* bi = reinterpret_cast<int64_t*>(base_items.ptr);
+    auto* bs = reinterpret_cast<int64_t*>(base_slots.ptr);
+    auto* bp = reinterpret_cast<int64_t*>(base_split.ptr);
+    if (W > 0) {
+        hipLaunchKernelGGL(plan_count, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
+                           d_window_offsets, d_window_order, W, set.seg, ci, cs, cp);
+        F3S_HIP(hipGetLastError());
+    }
+    auto* tp = reinterpret_cast<int64_t*>(tmp.ptr);
+    F3S_TRY(exclusive_scan_i32_to_i64(ci, bi, W, tp, st));
+    F3S_TRY(exclusive_scan_i32_to_i64(cs, bs, W, tp, st));
+    F3S_TRY(exclusive_scan_i32_to_i64(cp, bp, W, tp, st));
+    int64_t totals[3] = {0, 0, 0};
+    F3S_HIP(hipMemcpyAsync(&totals[0], bi + W, 8, hipMemcpyDeviceToHost, st));
+    F3S_HIP(hipMemcpyAsync(&totals[1], bs + W, 8, hipMemcpyDeviceToHost, st));
+    F3S_HIP(hipMemcpyAsync(&totals[2], bp + W, 8, hipMemcpyDeviceToHost, st));
+    F3S_HIP(hipStreamSynchronize(st));
+    set.num_items = totals[0];
+    set.num_slots = totals[1];
+    set.num_split = totals[2];
+    F3S_TRY(set.items.reserve(sizeof(Item) * (size_t)(set.num_items + 1)));
+    F3S_TRY(set.splits.reserve(sizeof(SplitInfo) * (size_t)(set.num_split + 1)));
+    F3S_TRY(set.partials.reserve(sizeof(float) * (size_t)kPartialFloats * H *
+                                 (size_t)(set.num_slots + 1)));
+    if (W > 0) {
+        hipLaunchKernelGGL(plan_fill, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
+                           d_window_offsets, d_window_order, W, set.seg, bi, bs, bp,
+                           reinterpret_cast<Item*>(set.items.ptr),
+                           reinterpret_cast<SplitInfo*>(set.splits.ptr));
+        F3S_HIP(hipGetLastError());
+    }
+    F3S_HIP(hipStreamSynchronize(st));
+    return F3S_OK;
+}
 
 static f3s_status check_attention_args(const void* Q, const void* K, const void* V, const void* O,
                                        int32_t n, int32_t d, int32_t H)
@@ -828,81 +892,36 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     clear_error();
     hipStream_t st = as_stream(stream);
 
-    f3s_plan* p = new f3s_plan();
-    p->W = W;
-    p->H = H;
-    p->natural_order = d_window_order == nullptr;
     int32_t T32 = 0;
     if (W > 0) {
         F3S_HIP(hipMemcpyAsync(&T32, d_window_offsets + W, sizeof T32, hipMemcpyDeviceToHost, st));
         F3S_HIP(hipStreamSynchronize(st));
     }
+    f3s_plan* p = new f3s_plan();
+    p->W = W;
+    p->H = H;
+    p->natural_order = d_window_order == nullptr;
     p->T = T32;
-    // Automatic segment size: enough segments that the heaviest item is a
-    // small fraction of one wave slot's share of the whole pass.
-    int64_t seg = seg_tiles;
-    if (seg == 0) {
-        // Small graphs are not split: a merge launch costs more than the
-        // serial tail it removes.
-        seg = ceil_div(p->T * H, 8192);
-        if (seg < 256) seg = 256;
+    // Automatic segment sizes: enough segments that the heaviest item is a
+    // small fraction of one wave slot's share of the pass (5,120 wave slots).
+    // Masked passes: small graphs are not split, since a merge launch costs
+    // more than the serial tail it removes; tile-dense passes: a segment is at
+    // most a tenth of a slot's share, and at least 16 tiles.
+    int64_t seg_m = seg_tiles, seg_d = 0;
+    if (seg_m == 0) {
+        seg_m = ceil_div(p->T * H, 8192);
+        if (seg_m < 256) seg_m = 256;
+        seg_d = ceil_div(p->T * H, 51200);
+        if (seg_d < 16) seg_d = 16;
+        if (seg_d >= seg_m) seg_d = 0;
     }
-    if (seg > INT32_MAX) seg = INT32_MAX;
-    p->seg = (int32_t)seg;
-
-    DeviceBuffer cnt_items, cnt_slots, cnt_split, base_items, base_slots, base_split, tmp;
-    auto fail = [&](f3s_status s) {
+    f3s_status s = build_items(p->masked, d_window_offsets, d_window_order, W, H, seg_m, st);
+    if (s == F3S_OK && seg_d > 0)
+        s = build_items(p->dense, d_window_offsets, d_window_order, W, H, seg_d, st);
+    if (s != F3S_OK) {
         delete p;
         return s;
-    };
-    f3s_status s;
-    if ((s = cnt_items.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
-        (s = cnt_slots.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
-        (s = cnt_split.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
-        (s = base_items.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
-        (s = base_slots.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
-        (s = base_split.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
-        (s = tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(W))) != F3S_OK)
-        return fail(s);
-    auto* ci = reinterpret_cast<int32_t*>(cnt_items.ptr);
-    auto* cs = reinterpret_cast<int32_t*>(cnt_slots.ptr);
-    auto* cp = reinterpret_cast<int32_t*>(cnt_split.ptr);
-    auto* bi = reinterpret_cast<int64_t*>(base_items.ptr);
-    auto* bs = reinterpret_cast<int64_t*>(base_slots.ptr);
-    auto* bp = reinterpret_cast<int64_t*>(base_split.ptr);
-    if (W > 0) {
-        hipLaunchKernelGGL(plan_count, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
-                           d_window_offsets, d_window_order, W, p->seg, ci, cs, cp);
-        if (hipGetLastError() != hipSuccess) return fail(F3S_EHIP);
     }
-    auto* tp = reinterpret_cast<int64_t*>(tmp.ptr);
-    if ((s = exclusive_scan_i32_to_i64(ci, bi, W, tp, st)) != F3S_OK ||
-        (s = exclusive_scan_i32_to_i64(cs, bs, W, tp, st)) != F3S_OK ||
-        (s = exclusive_scan_i32_to_i64(cp, bp, W, tp, st)) != F3S_OK)
-        return fail(s);
-    int64_t totals[3] = {0, 0, 0};
-    if (hipMemcpyAsync(&totals[0], bi + W, 8, hipMemcpyDeviceToHost, st) != hipSuccess ||
-        hipMemcpyAsync(&totals[1], bs + W, 8, hipMemcpyDeviceToHost, st) != hipSuccess ||
-        hipMemcpyAsync(&totals[2], bp + W, 8, hipMemcpyDeviceToHost, st) != hipSuccess ||
-        hipStreamSynchronize(st) != hipSuccess)
-        return fail(hip_fail(hipGetLastError(), "plan totals", __FILE__, __LINE__));
-    p->num_items = totals[0];
-    p->num_slots = totals[1];
-    p->num_split = totals[2];
-    if ((s = p->items.reserve(sizeof(Item) * (size_t)(p->num_items + 1))) != F3S_OK ||
-        (s = p->splits.reserve(sizeof(SplitInfo) * (size_t)(p->num_split + 1))) != F3S_OK ||
-        (s = p->partials.reserve(sizeof(float) * (size_t)kPartialFloats * H *
-                                 (size_t)(p->num_slots + 1))) != F3S_OK)
-        return fail(s);
-    if (W > 0) {
-        hipLaunchKernelGGL(plan_fill, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
-                           d_window_offsets, d_window_order, W, p->seg, bi, bs, bp,
-                           reinterpret_cast<Item*>(p->items.ptr),
-                           reinterpret_cast<SplitInfo*>(p->splits.ptr));
-        if (hipGetLastError() != hipSuccess) return fail(F3S_EHIP);
-    }
-    if (hipStreamSynchronize(st) != hipSuccess)
-        return fail(hip_fail(hipGetLastError(), "plan build", __FILE__, __LINE__));
     *plan_out = p;
     return F3S_OK;
 }
@@ -923,14 +942,14 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     plan->compiled_tile_mask = nullptr;
     plan->compiled_block_col = nullptr;
     plan->compiled_n = -1;
-    const int64_t ni = plan->num_items;
+    const int64_t ni = plan->masked.num_items;
     DeviceBuffer counts, tmp;
     F3S_TRY(counts.reserve(sizeof(int32_t) * (size_t)(ni + 1)));
     F3S_TRY(tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(ni)));
     DeviceBuffer base64;
     F3S_TRY(base64.reserve(sizeof(int64_t) * (size_t)(ni + 1)));
     const uint32_t row_stride = (uint32_t)plan->H * kRowBytes;
-    const auto* items = reinterpret_cast<const Item*>(plan->items.ptr);
+    const auto* items = reinterpret_cast<const Item*>(plan->masked.items.ptr);
     const dim3 grid((unsigned)ceil_div(ni > 0 ? ni : 1, 4));
     if (ni > 0)
         hipLaunchKernelGGL(plan_columns<false>, grid, dim3(256), 0, st, items, ni, d_block_col,
@@ -976,10 +995,10 @@ f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_
                          int64_t* T, int32_t* seg_tiles)
 {
     F3S_REQUIRE(plan != nullptr, "f3s_plan_info: NULL plan");
-    if (num_items) *num_items = plan->num_items;
-    if (num_split_windows) *num_split_windows = plan->num_split;
+    if (num_items) *num_items = plan->masked.num_items;
+    if (num_split_windows) *num_split_windows = plan->masked.num_split;
     if (T) *T = plan->T;
-    if (seg_tiles) *seg_tiles = plan->seg;
+    if (seg_tiles) *seg_tiles = plan->masked.seg;
     return F3S_OK;
 }
 
@@ -1005,14 +1024,16 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
     p.O = O;
     p.block_col = d_block_col;
     p.tile_mask = d_tile_mask;
-    p.items = reinterpret_cast<const Item*>(plan->items.ptr);
-    p.num_items = plan->num_items;
+    // tile-dense passes run the finer item set when the plan has one
+    const f3s_item_set& set = (!d_tile_mask && plan->dense.seg > 0) ? plan->dense : plan->masked;
+    p.items = reinterpret_cast<const Item*>(set.items.ptr);
+    p.num_items = set.num_items;
     p.W = plan->W;
     p.n = n;
     p.xcd_contiguous = plan->natural_order;
-    p.partials = reinterpret_cast<float*>(plan->partials.ptr);
-    p.splits = reinterpret_cast<const SplitInfo*>(plan->splits.ptr);
-    p.num_split = plan->num_split;
+    p.partials = reinterpret_cast<float*>(set.partials.ptr);
+    p.splits = reinterpret_cast<const SplitInfo*>(set.splits.ptr);
+    p.num_split = set.num_split;
     if (d_tile_mask && d_tile_mask == plan->compiled_tile_mask &&
         d_block_col == plan->compiled_block_col && n == plan->compiled_n) {
         p.chunk_base = reinterpret_cast<const int32_t*>(plan->chunk_base.ptr);

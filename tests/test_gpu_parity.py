@@ -297,6 +297,10 @@ def test_attention_hub_split_merge(gpu):
         for compiled in (False, True):
             got = p.run(True, planned=True, seg=seg, compiled=compiled)
             assert_close(got, want, f"star seg={seg} compiled={compiled}")
+    # tile-dense passes of an automatic plan run its finer item set
+    want_d = p.oracle(False)
+    for seg in (0, 64):
+        assert_close(p.run(False, planned=True, seg=seg), want_d, f"star tile-dense seg={seg}")
     got = p.run(True, planned=False)
     assert_close(got, want, "star unplanned")
 
