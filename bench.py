@@ -118,6 +118,9 @@ def main() -> int:
     ap.add_argument("--no-compile", action="store_true",
                     help="masked passes expand tiles on every pass instead of using the "
                          "plan's compiled column lists")
+    ap.add_argument("--heads", type=int, default=0,
+                    help="override the configuration's head count (1, 2 or 4); the line is "
+                         "then not the configuration's own workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run device-to-device copies of this size (calibrates the "
@@ -154,6 +157,9 @@ def main() -> int:
         return 0
     f3s.init()
     c = f3s.CONFIGS[args.config]
+    if args.heads:
+        import dataclasses
+        c = dataclasses.replace(c, H=args.heads)
     masked = args.semantics == "masked"
     t0 = time.time()
     rp, ci = c.graph()
@@ -221,7 +227,7 @@ def main() -> int:
     achieved = nbytes / (kavg * 1e-3) / 1e9
     flops_tile = bsf.T * 4 * 16 * 16 * d * H
     traffic = read_traffic(c.cfg, masked and not args.no_compile and args.order == "auto"
-                           and args.seg == 0)
+                           and args.seg == 0 and not args.heads)
     res = {
         "metric": "fused attention edges/s + kernel us; achieved HBM GB/s (% of peak) on 1 MI355X",
         "value": nnz * args.steps / wall,
@@ -235,7 +241,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f16 in, f32 accumulate/softmax/out",
         "data": "synthetic (seeded generator; no dataset download)",
-        "config": {"workload": f"cfg{c.cfg}: {c.name}", "nodes": n, "edges": nnz, "heads": H,
+        "config": {"workload": f"cfg{c.cfg}: {c.name}" + (f" with H={H}" if args.heads else ""), "nodes": n, "edges": nnz, "heads": H,
                    "head_dim": d, "semantics": args.semantics,
                    "window_order": "descending workload" if use_sorted else "natural",
                    "row_windows": bsf.W,
