@@ -343,35 +343,42 @@ fused_attention_kernel(const AttnParams p)
     if constexpr (MODE == kModeList) {
       {
         // ---- compiled plan: the attended columns were listed once per graph ----
-        // The chunk's 256-byte record (32 offsets, 32 row masks) is read with
-        // one coalesced load, lane l <- word l, one chunk ahead, and handed
-        // out through LDS: the vector-memory address path, not HBM, bounds
-        // this pass, so it gets one instruction instead of eight.
+        // Chunk records (32 offsets, 32 row masks: 256 bytes) are read four at
+        // a time with one coalesced 16-byte load per lane, one block ahead,
+        // and handed out through LDS: the vector-memory address path, not
+        // HBM, bounds this pass, so metadata costs a quarter instruction per
+        // chunk.  The plan pads its record array by four records, so a block
+        // read at an item's last chunks stays inside it.
         const int rbit = (r & 1) ? 16 + (r >> 1) : (r >> 1);
         const int64_t cb = p.chunk_base[item_idx], ce = p.chunk_base[item_idx + 1];
         const uint32_t piece_off = head_off + 16 * (lane & 7);
-        uint32_t* meta = reinterpret_cast<uint32_t*>(L.off);   // 64 words of this wave's ring
-        uint32_t word = cb < ce ? p.columns[cb * 64 + lane] : 0u;
-        for (int64_t c = cb; c < ce; ++c) {
-            F3S_WAVE_LDS_SYNC();   // the previous chunk's reads of meta are done
-            meta[lane] = word;
+        uint32_t* meta = reinterpret_cast<uint32_t*>(L.off);   // 4 records of this wave
+        const uint4* __restrict__ rec = reinterpret_cast<const uint4*>(p.columns);
+        uint4 blk = cb < ce ? rec[cb * 16 + lane] : make_uint4(0u, 0u, 0u, 0u);
+        for (int64_t c0 = cb; c0 < ce; c0 += 4) {
+            F3S_WAVE_LDS_SYNC();   // the previous block's reads of meta are done
+            *reinterpret_cast<uint4*>(&meta[4 * lane]) = blk;
             F3S_WAVE_LDS_SYNC();
-            if (c + 1 < ce) word = p.columns[(c + 1) * 64 + lane];   // next record, in flight
-            h8 krow[4], vrow[4];
+            if (c0 + 4 < ce) blk = rec[(c0 + 4) * 16 + lane];   // next block, in flight
+            const int nk = (int)min((int64_t)4, ce - c0);
+            for (int k = 0; k < nk; ++k) {
+                const uint32_t* m = meta + 64 * k;
+                h8 krow[4], vrow[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t o = meta[(lane >> 3) + 8 * i] + piece_off;
-                krow[i] = load_h8(kres, o);
-                vrow[i] = load_h8(vres, o);
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t o = m[(lane >> 3) + 8 * i] + piece_off;
+                    krow[i] = load_h8(kres, o);
+                    vrow[i] = load_h8(vres, o);
+                }
+                const uint4 ra = *reinterpret_cast<const uint4*>(&m[32 + 4 * g]);
+                const uint4 rb = *reinterpret_cast<const uint4*>(&m[48 + 4 * g]);
+                const uint32_t valid =
+                    ((ra.x >> rbit) & 1u) | (((ra.y >> rbit) & 1u) << 1) |
+                    (((ra.z >> rbit) & 1u) << 2) | (((ra.w >> rbit) & 1u) << 3) |
+                    (((rb.x >> rbit) & 1u) << 4) | (((rb.y >> rbit) & 1u) << 5) |
+                    (((rb.z >> rbit) & 1u) << 6) | (((rb.w >> rbit) & 1u) << 7);
+                chunk_step(st, krow, q0, q1, valid, vrow, L.stage, lane, p.scale_log2);
             }
-            const uint4 ra = *reinterpret_cast<const uint4*>(&meta[32 + 4 * g]);
-            const uint4 rb = *reinterpret_cast<const uint4*>(&meta[48 + 4 * g]);
-            const uint32_t valid =
-                ((ra.x >> rbit) & 1u) | (((ra.y >> rbit) & 1u) << 1) |
-                (((ra.z >> rbit) & 1u) << 2) | (((ra.w >> rbit) & 1u) << 3) |
-                (((rb.x >> rbit) & 1u) << 4) | (((rb.y >> rbit) & 1u) << 5) |
-                (((rb.z >> rbit) & 1u) << 6) | (((rb.w >> rbit) & 1u) << 7);
-            chunk_step(st, krow, q0, q1, valid, vrow, L.stage, lane, p.scale_log2);
         }
       }
     } else if constexpr (MODE == kModeRing) {
@@ -966,7 +973,8 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
         set_error("f3s_plan_compile: more than 2^31-1 chunks");
         return F3S_EUNSUPPORTED;
     }
-    F3S_TRY(plan->columns.reserve(sizeof(uint32_t) * 64 * (size_t)(total > 0 ? total : 1)));
+    // four records of padding: the pass reads records in blocks of four
+    F3S_TRY(plan->columns.reserve(sizeof(uint32_t) * 64 * (size_t)(total + 4)));
     F3S_TRY(plan->chunk_base.reserve(sizeof(int32_t) * (size_t)(ni + 1)));
     if (ni > 0) {
         hipLaunchKernelGGL(plan_columns<true>, grid, dim3(256), 0, st, items, ni, d_block_col,
