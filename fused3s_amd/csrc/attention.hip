@@ -538,26 +538,53 @@ __global__ void __launch_bounds__(256) merge_partials_kernel(const AttnParams p)
     auto part = [&](int k) {
         return p.partials + ((int64_t)(si.first_slot + k) * H + h) * kPartialFloats;
     };
-    float M = -INFINITY;
-    for (int k = 0; k < si.nseg; ++k) M = __builtin_fmaxf(M, part(k)[16 * kD + r]);
-    float Ls = 0.f;
+    // Online merge over the segments in slot order, eight segments' loads in
+    // flight at a time: a small graph's merge is otherwise a chain of
+    // dependent load latencies.  (m, l, O) of a batch are rescaled to the
+    // batch's running max, so one pass suffices.
+    float M = -INFINITY, Ls = 0.f;
     float4 o[4] = {make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0),
                    make_float4(0, 0, 0, 0)};
-    if (M != -INFINITY) {
-        for (int k = 0; k < si.nseg; ++k) {
-            const float* pk = part(k);
-            const float f = fast_exp2(pk[16 * kD + r] - M);
-            Ls += pk[16 * kD + 16 + r] * f;
+    constexpr int kB = 8;
+    for (int k0 = 0; k0 < si.nseg; k0 += kB) {
+        float mk[kB], lk[kB];
+        float4 a[kB][4];
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+            const bool in = k0 + j < si.nseg;
+            const float* pk = part(in ? k0 + j : k0);
+            mk[j] = in ? pk[16 * kD + r] : -INFINITY;
+            lk[j] = pk[16 * kD + 16 + r];
             const float* src = pk + r * kD + 16 * g;
 #pragma unroll
+            for (int v = 0; v < 4; ++v) a[j][v] = *reinterpret_cast<const float4*>(src + 4 * v);
+        }
+        float Mb = M;
+#pragma unroll
+        for (int j = 0; j < kB; ++j) Mb = __builtin_fmaxf(Mb, mk[j]);
+        if (Mb == -INFINITY) continue;   // all rows of these segments empty
+        const float c = fast_exp2(M - Mb);   // 0 while M is still -inf
+        Ls *= c;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            o[v].x *= c;
+            o[v].y *= c;
+            o[v].z *= c;
+            o[v].w *= c;
+        }
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+            const float f = fast_exp2(mk[j] - Mb);   // 0 for absent / empty segments
+            Ls += lk[j] * f;
+#pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float4 a = *reinterpret_cast<const float4*>(src + 4 * v);
-                o[v].x += a.x * f;
-                o[v].y += a.y * f;
-                o[v].z += a.z * f;
-                o[v].w += a.w * f;
+                o[v].x += a[j][v].x * f;
+                o[v].y += a[j][v].y * f;
+                o[v].z += a[j][v].z * f;
+                o[v].w += a[j][v].w * f;
             }
         }
+        M = Mb;
     }
     const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
     const int32_t row = si.w * 16 + r;
