@@ -41,6 +41,7 @@
 // assignment of k indices to (group, element) gives the same product; the
 // code relies only on that and on the row/column/C mapping.
 #include <math.h>
+#include <new>
 #include <stdio.h>
 
 #include "f3s_common.hpp"
@@ -931,7 +932,11 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
         F3S_HIP(hipMemcpyAsync(&T32, d_window_offsets + W, sizeof T32, hipMemcpyDeviceToHost, st));
         F3S_HIP(hipStreamSynchronize(st));
     }
-    f3s_plan* p = new f3s_plan();
+    f3s_plan* p = new (std::nothrow) f3s_plan();
+    if (!p) {
+        set_error("f3s_plan_create: out of host memory");
+        return F3S_ENOMEM;
+    }
     p->W = W;
     p->H = H;
     p->natural_order = d_window_order == nullptr;

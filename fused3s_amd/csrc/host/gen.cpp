@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -153,6 +154,21 @@ static int64_t count_unique_directed(int32_t n, const std::vector<int32_t>& pu,
 
 using namespace f3s_host;
 
+namespace {
+// Runs `body` (which returns 0 or 1); an exception (std::bad_alloc from a
+// large sample, say) becomes an error return instead of crossing the C ABI.
+template <typename F>
+int32_t guarded(const char* name, F&& body)
+{
+    try {
+        return body();
+    } catch (const std::exception& e) {
+        set_error(std::string(name) + ": " + e.what());
+        return 1;
+    }
+}
+}  // namespace
+
 extern "C" {
 
 int32_t f3s_gen_powerlaw(int32_t n, int64_t target_edges, double gamma, double max_degree,
@@ -163,6 +179,7 @@ int32_t f3s_gen_powerlaw(int32_t n, int64_t target_edges, double gamma, double m
         set_error("f3s_gen_powerlaw: bad arguments");
         return 1;
     }
+    return guarded("f3s_gen_powerlaw", [&]() -> int32_t {
     const double alpha = 1.0 / (gamma - 1.0);
     // Expected degree of node 0 relative to the total, from the integral of
     // x^-alpha (midpoint rule); bisection on the offset i0.
@@ -227,6 +244,7 @@ int32_t f3s_gen_powerlaw(int32_t n, int64_t target_edges, double gamma, double m
         S += (int64_t)ceil(((double)target_edges - (double)have) / per_sample);
     }
     return build_csr(n, pu, pv, self_loops != 0, row_ptr, col_idx, nnz);
+    });
 }
 
 int32_t f3s_gen_sbm(int32_t n, int32_t community, double mean_degree, double p_intra,
@@ -238,6 +256,7 @@ int32_t f3s_gen_sbm(int32_t n, int32_t community, double mean_degree, double p_i
         set_error("f3s_gen_sbm: bad arguments");
         return 1;
     }
+    return guarded("f3s_gen_sbm", [&]() -> int32_t {
     const int64_t S = (int64_t)((double)n * mean_degree / 2.0);
     std::vector<int32_t> pu(S), pv(S);
     const Stream es(seed, 2);
@@ -258,6 +277,7 @@ int32_t f3s_gen_sbm(int32_t n, int32_t community, double mean_degree, double p_i
         pv[k] = std::min(v, n - 1);
     }
     return build_csr(n, pu, pv, self_loops != 0, row_ptr, col_idx, nnz);
+    });
 }
 
 int32_t f3s_gen_features_f16(uint64_t seed, int32_t tensor, int64_t count, int32_t dist,

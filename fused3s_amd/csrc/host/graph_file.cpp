@@ -33,6 +33,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <stdexcept>
 #include <string>
 
 #include "../../../include/f3s_host.h"
@@ -124,12 +125,51 @@ struct File {
 
 }  // namespace
 
+// The entry points below catch what the C++ library may throw (allocation
+// failures in std::string) so that nothing crosses the C ABI.
+static int32_t save_impl(const char* path, int32_t n, int64_t nnz, const int32_t* row_ptr,
+                         const int32_t* col_idx, int32_t W, int64_t T,
+                         const int32_t* window_offsets, const int32_t* block_col,
+                         const uint16_t* tile_mask);
+static int32_t load_impl(const char* path, int32_t* n_out, int64_t* nnz_out, int32_t** row_ptr,
+                         int32_t** col_idx, int32_t* W_out, int64_t* T_out,
+                         int32_t** window_offsets, int32_t** block_col, uint16_t** tile_mask);
+
 extern "C" {
 
 int32_t f3s_host_save_graph(const char* path, int32_t n, int64_t nnz, const int32_t* row_ptr,
                             const int32_t* col_idx, int32_t W, int64_t T,
                             const int32_t* window_offsets, const int32_t* block_col,
                             const uint16_t* tile_mask)
+{
+    try {
+        return save_impl(path, n, nnz, row_ptr, col_idx, W, T, window_offsets, block_col,
+                         tile_mask);
+    } catch (const std::exception& e) {
+        set_error(std::string("f3s_host_save_graph: ") + e.what());
+        return 1;
+    }
+}
+
+int32_t f3s_host_load_graph(const char* path, int32_t* n_out, int64_t* nnz_out,
+                            int32_t** row_ptr, int32_t** col_idx, int32_t* W_out, int64_t* T_out,
+                            int32_t** window_offsets, int32_t** block_col, uint16_t** tile_mask)
+{
+    try {
+        return load_impl(path, n_out, nnz_out, row_ptr, col_idx, W_out, T_out, window_offsets,
+                         block_col, tile_mask);
+    } catch (const std::exception& e) {
+        set_error(std::string("f3s_host_load_graph: ") + e.what());
+        return 1;
+    }
+}
+
+}  // extern "C"
+
+static int32_t save_impl(const char* path, int32_t n, int64_t nnz, const int32_t* row_ptr,
+                         const int32_t* col_idx, int32_t W, int64_t T,
+                         const int32_t* window_offsets, const int32_t* block_col,
+                         const uint16_t* tile_mask)
 {
     if (!path || n < 0 || nnz < 0 || !row_ptr || (nnz > 0 && !col_idx)) {
         set_error("f3s_host_save_graph: bad CSR arguments");
@@ -192,9 +232,9 @@ int32_t f3s_host_save_graph(const char* path, int32_t n, int64_t nnz, const int3
     return 0;
 }
 
-int32_t f3s_host_load_graph(const char* path, int32_t* n_out, int64_t* nnz_out,
-                            int32_t** row_ptr, int32_t** col_idx, int32_t* W_out, int64_t* T_out,
-                            int32_t** window_offsets, int32_t** block_col, uint16_t** tile_mask)
+static int32_t load_impl(const char* path, int32_t* n_out, int64_t* nnz_out,
+                         int32_t** row_ptr, int32_t** col_idx, int32_t* W_out, int64_t* T_out,
+                         int32_t** window_offsets, int32_t** block_col, uint16_t** tile_mask)
 {
     if (!path || !n_out || !nnz_out || !row_ptr || !col_idx || !W_out || !T_out ||
         !window_offsets || !block_col || !tile_mask) {
@@ -318,4 +358,4 @@ int32_t f3s_host_load_graph(const char* path, int32_t* n_out, int64_t* nnz_out,
     return 0;
 }
 
-}  // extern "C"
+

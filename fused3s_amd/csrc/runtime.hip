@@ -11,7 +11,13 @@ namespace f3s {
 
 static thread_local std::string g_last_error;
 
-void set_error(const std::string& msg) { g_last_error = msg; }
+void set_error(const std::string& msg)
+{
+    try {
+        g_last_error = msg;
+    } catch (...) {   // keep the old message rather than throw across the C ABI
+    }
+}
 void clear_error() { g_last_error.clear(); }
 
 f3s_status hip_fail(hipError_t err, const char* what, const char* file, int line)
