@@ -119,7 +119,7 @@ def main() -> int:
                     help="masked passes expand tiles on every pass instead of using the "
                          "plan's compiled column lists")
     ap.add_argument("--heads", type=int, default=0,
-                    help="override the configuration's head count (1, 2 or 4); the line is "
+                    help="override the configuration's head count (1 to 64); the line is "
                          "then not the configuration's own workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,

@@ -60,6 +60,7 @@ constexpr int kChunk = 32;         // attended columns per MFMA step
 constexpr int kRing = 256;         // column ring entries per wave
 constexpr int kPartialFloats = 16 * kD + 32;   // O[16][64], m[16], l[16]
 constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
+constexpr int kMaxHeads = 64;
 // Word 3 of a raw buffer descriptor for the gfx9 family (incl. gfx950):
 // 32-bit data format, no swizzle.  Offsets >= num_records read as 0.
 constexpr int32_t kBufferFlags = 0x00020000;
@@ -95,6 +96,7 @@ struct AttnParams {
     const Item* items;               // planned launch (NULL: one item per window)
     int64_t num_items;
     int32_t W, n;
+    int32_t H;                       // heads, 1 <= H <= kMaxHeads
     float scale_log2;
     int32_t xcd_contiguous;          // map consecutive items to the same XCD
     uint32_t feat_bytes;             // bytes of Q (= K = V), < 2^32
@@ -288,10 +290,11 @@ enum Mode : int {
 // chunk's gathers in flight per wave (double-buffered registers, 3 waves per
 // SIMD) measured no faster than one chunk per wave at 4-5 waves per SIMD, so
 // the simpler single-buffered loop is kept.
-template <int H, int MODE, int WPG>
+template <int MODE, int WPG>
 __global__ void __launch_bounds__(kWave * WPG) __attribute__((amdgpu_waves_per_eu(4)))
 fused_attention_kernel(const AttnParams p)
 {
+    const int H = p.H;
     __shared__ WaveLds lds_all[WPG];
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
@@ -300,9 +303,10 @@ fused_attention_kernel(const AttnParams p)
     WaveLds& L = lds_all[wave];
 
     const int32_t n = p.n;
-    const int64_t gw = logical_block(p.xcd_contiguous) * WPG + wave;
-    const int64_t item_idx = gw / H;
-    const int h = (int)(gw % H);
+    // wave -> (item, head); the launch keeps num_items * H < 2^31
+    const uint32_t gw = (uint32_t)(logical_block(p.xcd_contiguous) * WPG + wave);
+    const int64_t item_idx = (int64_t)(gw / (uint32_t)H);
+    const int h = (int)(gw % (uint32_t)H);
     if (item_idx >= p.num_items) return;
 
     // ---- item decode (wave-uniform) ----
@@ -526,14 +530,14 @@ fused_attention_kernel(const AttnParams p)
 // Combines the segments of each split window, in slot order (deterministic):
 // M = max m_k, O = sum O_k 2^(m_k - M) / sum l_k 2^(m_k - M).  One wave per
 // (split window, head); lane (g, r) owns row r, dims 16g..16g+15.
-template <int H>
 __global__ void __launch_bounds__(256) merge_partials_kernel(const AttnParams p)
 {
-    const int64_t gw = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    const int H = p.H;
+    const uint32_t gw = blockIdx.x * 4u + threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
     const int g = lane >> 4, r = lane & 15;
-    const int64_t sid = gw / H;
-    const int h = (int)(gw % H);
+    const int64_t sid = (int64_t)(gw / (uint32_t)H);
+    const int h = (int)(gw % (uint32_t)H);
     if (sid >= p.num_split) return;
     const SplitInfo si = p.splits[sid];
     auto part = [&](int k) {
@@ -820,8 +824,8 @@ static f3s_status check_attention_args(const void* Q, const void* K, const void*
         set_error("attention: only d == 64 is implemented (FEAT_DIM_FIXED of the reference)");
         return F3S_EUNSUPPORTED;
     }
-    if (H != 1 && H != 2 && H != 4) {
-        set_error("attention: H must be 1, 2 or 4");
+    if (H < 1 || H > kMaxHeads) {
+        set_error("attention: H must be in [1, 64]");
         return F3S_EUNSUPPORTED;
     }
     F3S_REQUIRE(n == 0 || (Q && K && V && O), "attention: NULL feature pointer");
@@ -834,31 +838,20 @@ static f3s_status check_attention_args(const void* Q, const void* K, const void*
     return F3S_OK;
 }
 
-template <int H, int MODE>
-static void launch_hm(const AttnParams& p, int64_t waves, hipStream_t st)
+template <int MODE>
+static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
 {
     // Small launches use one-wave workgroups so they spread over all CUs.
     if (waves < 4 * 256 * 2) {
-        hipLaunchKernelGGL((fused_attention_kernel<H, MODE, 1>), dim3((unsigned)waves),
+        hipLaunchKernelGGL((fused_attention_kernel<MODE, 1>), dim3((unsigned)waves),
                            dim3(kWave), 0, st, p);
     } else {
-        hipLaunchKernelGGL((fused_attention_kernel<H, MODE, 4>),
+        hipLaunchKernelGGL((fused_attention_kernel<MODE, 4>),
                            dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
     }
     if (p.num_split > 0)
-        hipLaunchKernelGGL(merge_partials_kernel<H>, dim3((unsigned)ceil_div(p.num_split * H, 4)),
-                           dim3(256), 0, st, p);
-}
-
-template <int H>
-static void launch_h(const AttnParams& p, int64_t waves, hipStream_t st)
-{
-    if (!p.tile_mask)
-        launch_hm<H, kModeDense>(p, waves, st);
-    else if (p.chunk_base)
-        launch_hm<H, kModeList>(p, waves, st);
-    else
-        launch_hm<H, kModeRing>(p, waves, st);
+        hipLaunchKernelGGL(merge_partials_kernel,
+                           dim3((unsigned)ceil_div(p.num_split * p.H, 4)), dim3(256), 0, st, p);
 }
 
 static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
@@ -868,12 +861,13 @@ static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
     F3S_REQUIRE(waves < ((int64_t)1 << 31), "attention: too many work items");
     p.scale_log2 = scale * 1.4426950408889634f;
     p.feat_bytes = (uint32_t)((int64_t)p.n * H * kRowBytes);
-    if (H == 1)
-        launch_h<1>(p, waves, st);
-    else if (H == 2)
-        launch_h<2>(p, waves, st);
+    p.H = H;
+    if (!p.tile_mask)
+        launch_m<kModeDense>(p, waves, st);
+    else if (p.chunk_base)
+        launch_m<kModeList>(p, waves, st);
     else
-        launch_h<4>(p, waves, st);
+        launch_m<kModeRing>(p, waves, st);
     F3S_HIP(hipGetLastError());
     return F3S_OK;
 }
@@ -921,7 +915,7 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     *plan_out = nullptr;
     F3S_REQUIRE(W >= 0, "f3s_plan_create: negative W");
     F3S_REQUIRE(W == 0 || d_window_offsets, "f3s_plan_create: NULL window_offsets");
-    F3S_REQUIRE(H == 1 || H == 2 || H == 4, "f3s_plan_create: H must be 1, 2 or 4");
+    F3S_REQUIRE(H >= 1 && H <= kMaxHeads, "f3s_plan_create: H must be in [1, 64]");
     F3S_REQUIRE(seg_tiles >= 0, "f3s_plan_create: negative seg_tiles");
     F3S_TRY(require_device());
     clear_error();

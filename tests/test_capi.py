@@ -51,8 +51,9 @@ def test_validation_happens_before_device_access():
     # d != 64 and bad H are rejected with F3S_EUNSUPPORTED on any host
     assert h.f3s_attention_fwd(None, None, None, None, None, None, None, None,
                                1, 16, 32, 1, 1.0, None) == 5
-    assert h.f3s_attention_fwd(None, None, None, None, None, None, None, None,
-                               1, 16, 64, 3, 1.0, None) == 5
+    for bad_h in (0, 65):
+        assert h.f3s_attention_fwd(None, None, None, None, None, None, None, None,
+                                   1, 16, 64, bad_h, 1.0, None) == 5
     # misaligned pointers are F3S_EINVAL
     assert h.f3s_attention_fwd(8, 16, 16, 16, 16, 16, None, None, 1, 16, 64, 1, 1.0, None) == 1
     T = C.c_int64()

@@ -276,7 +276,7 @@ def test_attention_configs_small(gpu, cfg, masked):
                                 f"compiled={compiled}")
 
 
-@pytest.mark.parametrize("H", [1, 2, 4])
+@pytest.mark.parametrize("H", [1, 2, 3, 4, 8])
 @pytest.mark.parametrize("n,deg,seed", [(1, 0, 1), (37, 5, 2), (500, 12, 3), (2050, 60, 4)])
 def test_attention_random_heads(gpu, H, n, deg, seed):
     rp, ci = random_csr(n, deg, seed, self_loops=(seed % 2 == 0))
@@ -344,7 +344,7 @@ def test_attention_rejects_bad_args(gpu):
         gpu.attention_fwd(p.dQ, p.dK, p.dV, p.dO, p.bsf, H=1, d=32)
     assert e.value.name == "F3S_EUNSUPPORTED"
     with pytest.raises(gpu.F3SError) as e:
-        gpu.attention_fwd(p.dQ, p.dK, p.dV, p.dO, p.bsf, H=3)
+        gpu.attention_fwd(p.dQ, p.dK, p.dV, p.dO, p.bsf, H=65)
     assert e.value.name == "F3S_EUNSUPPORTED"
 
 
