@@ -178,9 +178,11 @@ __device__ __forceinline__ float row_max4(float x)
 // 4g..4g+3, then tile 1 rows 16+4g..16+4g+3.  Used as the k order of P.V.
 __device__ __forceinline__ int slot_of(int g, int j) { return (j < 4) ? 4 * g + j : 16 + 4 * g + (j - 4); }
 
-// Out-of-range buffer offset: loads read 0 (and a few added bytes cannot
-// wrap past 2^32, since the buffers are smaller than 2^32 - 512 bytes).
-constexpr uint32_t kNoRow = 0xffffff00u;
+// Out-of-range buffer offset for slots with no row: loads read 0.  The
+// largest offset added to it (head offset + piece + 64 for Q's second half,
+// under 8,256 bytes at 64 heads) cannot wrap past 2^32, and the feature
+// tensors are required to end at or below it.
+constexpr uint32_t kNoRow = 0xffffc000u;
 
 // Online-softmax state of one row (lane (g, r) holds row r).  The running
 // max m (log2 domain) is moved only when a chunk's max exceeds it by more
@@ -831,7 +833,7 @@ static f3s_status check_attention_args(const void* Q, const void* K, const void*
     F3S_REQUIRE(n == 0 || (Q && K && V && O), "attention: NULL feature pointer");
     F3S_REQUIRE(((((uintptr_t)Q) | ((uintptr_t)K) | ((uintptr_t)V) | ((uintptr_t)O)) & 15) == 0,
                 "attention: Q, K, V, O must be 16-byte aligned");
-    if ((int64_t)n * H * kRowBytes >= ((int64_t)1 << 32) - 512) {
+    if ((int64_t)n * H * kRowBytes > (int64_t)kNoRow) {
         set_error("attention: Q/K/V larger than 4 GiB are not supported (32-bit buffer offsets)");
         return F3S_EUNSUPPORTED;
     }

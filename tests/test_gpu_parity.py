@@ -337,6 +337,34 @@ def test_attention_deterministic(gpu):
     assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
 
 
+@pytest.mark.parametrize("H", [4, 8])
+def test_padding_slots_read_nothing(gpu, H):
+    # Chunk padding must read zeros, never a real row: with V of node 0 set
+    # to NaN, only windows that gather node 0 may see it (a gathered column
+    # is shared by the window's rows, and 0 * NaN is NaN).  A padding offset
+    # plus a large head offset once wrapped around 2^32 onto node 0's row.
+    rp, ci = random_csr(700, 7, 31)
+    p = Problem(gpu, rp, ci, H=H, normal=True, seed=31)
+    p.V[0] = np.float16(np.nan)
+    p.Vf = p.V.astype(np.float32)
+    p.dV.upload(p.V.view(np.uint16))
+    n = p.n
+    rows = np.repeat(np.arange(n), np.diff(rp))
+    touched = np.zeros((n + 15) // 16, bool)
+    touched[rows[ci == 0] // 16] = True               # masked: a row attends node 0
+    for masked in (True, False):
+        want = p.oracle(masked)
+        win = touched if masked else ~np.isfinite(want).reshape(n, -1).all(1)[::16]
+        ok = ~np.repeat(win, 16)[:n]
+        assert ok.any() and not ok.all()
+        for planned, compiled in ((False, False), (True, False), (True, True)):
+            got = p.run(masked, planned=planned, compiled=compiled and masked)
+            assert np.all(np.isfinite(got[ok])), f"H={H} masked={masked} planned={planned}"
+            assert np.all(np.isfinite(want[ok]))
+            mabs = float(np.abs(got[ok] - want[ok]).max())
+            assert mabs <= ABS_TOL, f"H={H} masked={masked} planned={planned}: {mabs}"
+
+
 def test_attention_rejects_bad_args(gpu):
     rp, ci = random_csr(40, 3, 1)
     p = Problem(gpu, rp, ci)
