@@ -99,7 +99,7 @@ struct AttnParams {
     int32_t H;                       // heads, 1 <= H <= kMaxHeads
     float scale_log2;
     int32_t xcd_contiguous;          // map consecutive items to the same XCD
-    uint32_t feat_bytes;             // bytes of Q (= K = V), < 2^32
+    uint32_t feat_bytes;             // bytes of Q (= K = V) in a narrow launch, else 0
     float* partials;
     const SplitInfo* splits;
     int64_t num_split;
@@ -183,6 +183,26 @@ __device__ __forceinline__ int slot_of(int g, int j) { return (j < 4) ? 4 * g + 
 // under 8,256 bytes at 64 heads) cannot wrap past 2^32, and the feature
 // tensors are required to end at or below it.
 constexpr uint32_t kNoRow = 0xffffc000u;
+// Wide launches (feature tensors beyond kNoRow bytes) address rows by node
+// index with 64-bit loads; kNoIdx marks a slot with no row.
+constexpr uint32_t kNoIdx = 0xffffffffu;
+
+// A row reference is the node's byte offset (node * row stride) in a narrow
+// launch and the node index in a wide one; `extra` adds the head and piece.
+template <bool WIDE>
+__device__ __forceinline__ h8 load_ref(__amdgpu_buffer_rsrc_t rs, const _Float16* base,
+                                       uint32_t ref, uint32_t row_stride, uint32_t extra)
+{
+    if constexpr (!WIDE) {
+        return load_h8(rs, ref + extra);
+    } else {
+        h8 v = {};
+        if (ref != kNoIdx)
+            v = *reinterpret_cast<const h8*>(reinterpret_cast<const char*>(base) +
+                                             (uint64_t)ref * row_stride + extra);
+        return v;
+    }
+}
 
 // Online-softmax state of one row (lane (g, r) holds row r).  The running
 // max m (log2 domain) is moved only when a chunk's max exceeds it by more
@@ -292,7 +312,7 @@ enum Mode : int {
 // chunk's gathers in flight per wave (double-buffered registers, 3 waves per
 // SIMD) measured no faster than one chunk per wave at 4-5 waves per SIMD, so
 // the simpler single-buffered loop is kept.
-template <int MODE, int WPG>
+template <int MODE, int WPG, bool WIDE>
 __global__ void __launch_bounds__(kWave * WPG) __attribute__((amdgpu_waves_per_eu(4)))
 fused_attention_kernel(const AttnParams p)
 {
@@ -334,12 +354,14 @@ fused_attention_kernel(const AttnParams p)
     const __amdgpu_buffer_rsrc_t vres = make_rsrc(p.V, p.feat_bytes);
     const uint32_t head_off = (uint32_t)h * kRowBytes;
     const uint32_t row_stride = H * kRowBytes;
+    const uint32_t ref_stride = WIDE ? 1u : row_stride;   // node -> row reference
+    const uint32_t no_ref = WIDE ? kNoIdx : kNoRow;
 
     // ---- Q tile in registers, B-operand layout ----
     const int32_t qrow = w * 16 + r;
-    const uint32_t qoff = qrow < n ? (uint32_t)qrow * row_stride + head_off + 16 * g : kNoRow;
-    const h8 q0 = load_h8(qres, qoff);
-    const h8 q1 = load_h8(qres, qoff + 64);
+    const uint32_t qref = qrow < n ? (uint32_t)qrow * ref_stride : no_ref;
+    const h8 q0 = load_ref<WIDE>(qres, p.Q, qref, row_stride, head_off + 16 * g);
+    const h8 q1 = load_ref<WIDE>(qres, p.Q, qref, row_stride, head_off + 16 * g + 64);
 
     RowState st;
     st.m = -INFINITY;
@@ -373,9 +395,9 @@ fused_attention_kernel(const AttnParams p)
                 h8 krow[4], vrow[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint32_t o = m[(lane >> 3) + 8 * i] + piece_off;
-                    krow[i] = load_h8(kres, o);
-                    vrow[i] = load_h8(vres, o);
+                    const uint32_t ref = m[(lane >> 3) + 8 * i];
+                    krow[i] = load_ref<WIDE>(kres, p.K, ref, row_stride, piece_off);
+                    vrow[i] = load_ref<WIDE>(vres, p.V, ref, row_stride, piece_off);
                 }
                 const uint4 ra = *reinterpret_cast<const uint4*>(&m[32 + 4 * g]);
                 const uint4 rb = *reinterpret_cast<const uint4*>(&m[48 + 4 * g]);
@@ -424,12 +446,12 @@ fused_attention_kernel(const AttnParams p)
                 const int added = __builtin_amdgcn_readlane(incl, nacc - 1);
                 if (accept && occ) {
                     int32_t pos = tail + incl - occ;
-                    const uint32_t base = (uint32_t)bc * 16 * row_stride + head_off;
+                    const uint32_t base = (uint32_t)bc * 16 * ref_stride;
                     uint32_t rest = u;
                     while (rest) {
                         const int c = __ffs(rest) - 1;
                         rest &= rest - 1;
-                        L.off[pos & kMask] = base + (uint32_t)c * row_stride;
+                        L.off[pos & kMask] = base + (uint32_t)c * ref_stride;
                         L.rm[pos & kMask] = column_rows(wd, c);
                         ++pos;
                     }
@@ -442,7 +464,7 @@ fused_attention_kernel(const AttnParams p)
             if (pending < kChunk && lane < kChunk - pending) {
                 // last, partial chunk: pad with slots nobody attends, whose
                 // loads fall outside the buffers and read as zero
-                L.off[(tail + lane) & kMask] = kNoRow;
+                L.off[(tail + lane) & kMask] = no_ref;
                 L.rm[(tail + lane) & kMask] = 0u;
             }
             F3S_WAVE_LDS_SYNC();
@@ -451,11 +473,12 @@ fused_attention_kernel(const AttnParams p)
             const uint32_t* off = &L.off[head & kMask];
             const uint32_t* rmr = &L.rm[head & kMask];
             h8 krow[4], vrow[4];
+            const uint32_t piece_off = head_off + 16 * (lane & 7);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t o = off[(lane >> 3) + 8 * i] + 16 * (lane & 7);
-                krow[i] = load_h8(kres, o);
-                vrow[i] = load_h8(vres, o);
+                const uint32_t ref = off[(lane >> 3) + 8 * i];
+                krow[i] = load_ref<WIDE>(kres, p.K, ref, row_stride, piece_off);
+                vrow[i] = load_ref<WIDE>(vres, p.V, ref, row_stride, piece_off);
             }
             const uint4 ra = *reinterpret_cast<const uint4*>(&rmr[4 * g]);
             const uint4 rb = *reinterpret_cast<const uint4*>(&rmr[16 + 4 * g]);
@@ -476,16 +499,16 @@ fused_attention_kernel(const AttnParams p)
             const bool ok0 = (uint32_t)bc0 < (uint32_t)nbc, ok1 = (uint32_t)bc1 < (uint32_t)nbc;
             const int32_t c0 = 16 * bc0, c1 = 16 * bc1;
             auto row_at = [&](bool ok, int32_t c, int s) -> uint32_t {
-                return ok && c + s < n ? (uint32_t)(c + s) * row_stride + head_off : kNoRow;
+                return ok && c + s < n ? (uint32_t)(c + s) * ref_stride : no_ref;
             };
             h8 krow[4], vrow[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int s = (lane >> 3) + 8 * i;   // slots 0-15: tile t, 16-31: tile t+1
-                const uint32_t o = (s < 16 ? row_at(ok0, c0, s) : row_at(ok1, c1, s - 16)) +
-                                   16 * (lane & 7);
-                krow[i] = load_h8(kres, o);
-                vrow[i] = load_h8(vres, o);
+                const uint32_t ref = s < 16 ? row_at(ok0, c0, s) : row_at(ok1, c1, s - 16);
+                const uint32_t extra = head_off + 16 * (lane & 7);
+                krow[i] = load_ref<WIDE>(kres, p.K, ref, row_stride, extra);
+                vrow[i] = load_ref<WIDE>(vres, p.V, ref, row_stride, extra);
             }
             // logit j of the lane is column 4g + j of tile t (j < 4) or
             // 4g + j - 4 of tile t+1; attended iff the column exists
@@ -677,7 +700,7 @@ template <bool FILL>
 __global__ void __launch_bounds__(256)
 plan_columns(const Item* __restrict__ items, int64_t num_items,
              const int32_t* __restrict__ block_col, const uint16_t* __restrict__ tile_mask,
-             int32_t n, uint32_t row_stride, int32_t* __restrict__ nchunks,
+             int32_t n, uint32_t ref_stride, uint32_t no_ref, int32_t* __restrict__ nchunks,
              const int64_t* __restrict__ chunk_base, uint32_t* __restrict__ columns)
 {
     const int64_t it = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
@@ -709,13 +732,13 @@ plan_columns(const Item* __restrict__ items, int64_t num_items,
         const int incl = wave_scan_incl(occ);
         if (FILL && occ) {
             int64_t q = pos + incl - occ;
-            const uint32_t base = (uint32_t)bc * 16 * row_stride;
+            const uint32_t base = (uint32_t)bc * 16 * ref_stride;
             uint32_t rest = u;
             while (rest) {
                 const int c = __ffs(rest) - 1;
                 rest &= rest - 1;
                 uint32_t* rec = rec0 + (q >> 5) * 64;
-                rec[q & 31] = base + (uint32_t)c * row_stride;
+                rec[q & 31] = base + (uint32_t)c * ref_stride;
                 rec[32 + (q & 31)] = column_rows(wd, c);
                 ++q;
             }
@@ -730,7 +753,7 @@ plan_columns(const Item* __restrict__ items, int64_t num_items,
     // pad the last chunk with slots no row attends, read as zero
     for (int64_t q = pos + lane; q < nch * kChunk; q += kWave) {
         uint32_t* rec = rec0 + (q >> 5) * 64;
-        rec[q & 31] = kNoRow;
+        rec[q & 31] = no_ref;
         rec[32 + (q & 31)] = 0u;
     }
 }
@@ -818,6 +841,13 @@ static f3s_status build_items(f3s_item_set& set, const int32_t* d_window_offsets
     return F3S_OK;
 }
 
+// Feature tensors whose bytes exceed the 32-bit offset range of the narrow
+// path (kNoRow, just under 4 GiB) are addressed with 64-bit loads.
+static bool wide_features(int32_t n, int32_t H)
+{
+    return (int64_t)n * H * kRowBytes > (int64_t)kNoRow;
+}
+
 static f3s_status check_attention_args(const void* Q, const void* K, const void* V, const void* O,
                                        int32_t n, int32_t d, int32_t H)
 {
@@ -833,27 +863,32 @@ static f3s_status check_attention_args(const void* Q, const void* K, const void*
     F3S_REQUIRE(n == 0 || (Q && K && V && O), "attention: NULL feature pointer");
     F3S_REQUIRE(((((uintptr_t)Q) | ((uintptr_t)K) | ((uintptr_t)V) | ((uintptr_t)O)) & 15) == 0,
                 "attention: Q, K, V, O must be 16-byte aligned");
-    if ((int64_t)n * H * kRowBytes > (int64_t)kNoRow) {
-        set_error("attention: Q/K/V larger than 4 GiB are not supported (32-bit buffer offsets)");
-        return F3S_EUNSUPPORTED;
-    }
     return F3S_OK;
 }
 
-template <int MODE>
-static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
+template <int MODE, bool WIDE>
+static void launch_mw(const AttnParams& p, int64_t waves, hipStream_t st)
 {
     // Small launches use one-wave workgroups so they spread over all CUs.
     if (waves < 4 * 256 * 2) {
-        hipLaunchKernelGGL((fused_attention_kernel<MODE, 1>), dim3((unsigned)waves),
+        hipLaunchKernelGGL((fused_attention_kernel<MODE, 1, WIDE>), dim3((unsigned)waves),
                            dim3(kWave), 0, st, p);
     } else {
-        hipLaunchKernelGGL((fused_attention_kernel<MODE, 4>),
+        hipLaunchKernelGGL((fused_attention_kernel<MODE, 4, WIDE>),
                            dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
     }
     if (p.num_split > 0)
         hipLaunchKernelGGL(merge_partials_kernel,
                            dim3((unsigned)ceil_div(p.num_split * p.H, 4)), dim3(256), 0, st, p);
+}
+
+template <int MODE>
+static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
+{
+    if (wide_features(p.n, p.H))
+        launch_mw<MODE, true>(p, waves, st);
+    else
+        launch_mw<MODE, false>(p, waves, st);
 }
 
 static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
@@ -862,8 +897,10 @@ static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
     const int64_t waves = p.num_items * H;
     F3S_REQUIRE(waves < ((int64_t)1 << 31), "attention: too many work items");
     p.scale_log2 = scale * 1.4426950408889634f;
-    p.feat_bytes = (uint32_t)((int64_t)p.n * H * kRowBytes);
     p.H = H;
+    // narrow launches range-check buffer loads against the tensor size;
+    // wide ones never use the buffer descriptors
+    p.feat_bytes = wide_features(p.n, H) ? 0u : (uint32_t)((int64_t)p.n * H * kRowBytes);
     if (!p.tile_mask)
         launch_m<kModeDense>(p, waves, st);
     else if (p.chunk_base)
@@ -969,8 +1006,6 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     F3S_REQUIRE(plan->T == 0 || d_block_col, "f3s_plan_compile: NULL block_col");
     F3S_REQUIRE((((uintptr_t)d_tile_mask) & 15) == 0, "f3s_plan_compile: tile_mask alignment");
     F3S_REQUIRE(plan->W == (int32_t)ceil_div(n, 16), "f3s_plan_compile: n does not match W");
-    F3S_REQUIRE((int64_t)n * plan->H * kRowBytes < ((int64_t)1 << 32) - 512,
-                "f3s_plan_compile: features larger than 4 GiB");
     F3S_TRY(require_device());
     clear_error();
     hipStream_t st = as_stream(stream);
@@ -983,13 +1018,17 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     F3S_TRY(tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(ni)));
     DeviceBuffer base64;
     F3S_TRY(base64.reserve(sizeof(int64_t) * (size_t)(ni + 1)));
-    const uint32_t row_stride = (uint32_t)plan->H * kRowBytes;
+    // the records hold row references: byte offsets, or node indices when the
+    // feature tensors are too large for 32-bit offsets (wide launches)
+    const bool wide = wide_features(n, plan->H);
+    const uint32_t ref_stride = wide ? 1u : (uint32_t)plan->H * kRowBytes;
+    const uint32_t no_ref = wide ? kNoIdx : kNoRow;
     const auto* items = reinterpret_cast<const Item*>(plan->masked.items.ptr);
     const dim3 grid((unsigned)ceil_div(ni > 0 ? ni : 1, 4));
     if (ni > 0)
         hipLaunchKernelGGL(plan_columns<false>, grid, dim3(256), 0, st, items, ni, d_block_col,
-                           d_tile_mask, n, row_stride, reinterpret_cast<int32_t*>(counts.ptr),
-                           nullptr, nullptr);
+                           d_tile_mask, n, ref_stride, no_ref,
+                           reinterpret_cast<int32_t*>(counts.ptr), nullptr, nullptr);
     F3S_HIP(hipGetLastError());
     auto* b64 = reinterpret_cast<int64_t*>(base64.ptr);
     F3S_TRY(exclusive_scan_i32_to_i64(reinterpret_cast<const int32_t*>(counts.ptr), b64, ni,
@@ -1006,7 +1045,7 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     F3S_TRY(plan->chunk_base.reserve(sizeof(int32_t) * (size_t)(ni + 1)));
     if (ni > 0) {
         hipLaunchKernelGGL(plan_columns<true>, grid, dim3(256), 0, st, items, ni, d_block_col,
-                           d_tile_mask, n, row_stride, nullptr, b64,
+                           d_tile_mask, n, ref_stride, no_ref, nullptr, b64,
                            reinterpret_cast<uint32_t*>(plan->columns.ptr));
         F3S_HIP(hipGetLastError());
     }

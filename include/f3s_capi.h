@@ -114,8 +114,9 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * handled whole, windows taken in d_window_order (NULL = natural order).
  * O[i] = sum_j softmax_j(scale * Q[i].K[j]) V[j] per head; rows with no
  * attended column get 0.  Requires d == 64 and 1 <= H <= 64 heads in
- * node-major [n][H][64] layout with n * H * 128 bytes < 4 GiB; scale = 1
- * reproduces the reference (which has no scaling, and one head). */
+ * node-major [n][H][64] layout, of any size (tensors past ~4 GiB are read
+ * with 64-bit addresses); scale = 1 reproduces the reference (which has no
+ * scaling, and one head). */
 f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                              float* O, const int32_t* d_window_offsets,
                              const int32_t* d_block_col, const uint16_t* d_tile_mask,
