@@ -12,7 +12,8 @@ from .device import (DeviceArray, Event, F3SError, Stream, device_count, device_
 from .graph import (BlockSparseFormat, DeviceBSF, DeviceCSR, GraphData, bsf_stats,
                     convert_csr_to_block_sparse, convert_device, generate_balanced_window_order,
                     load_csr_graph, load_graph, save_graph, window_order_device)
-from .attention import Plan, attention_fwd, cast_f32_to_f16, naive_attention_fwd
+from .attention import (Plan, attention_fwd, attention_fwd_timed, cast_f32_to_f16,
+                        naive_attention_fwd)
 from .configs import CONFIGS, Config
 
 __all__ = [
@@ -21,6 +22,6 @@ __all__ = [
     "BlockSparseFormat", "DeviceBSF", "DeviceCSR", "GraphData", "bsf_stats",
     "convert_csr_to_block_sparse", "convert_device", "generate_balanced_window_order",
     "load_csr_graph", "load_graph", "save_graph", "window_order_device", "Plan",
-    "attention_fwd", "cast_f32_to_f16", "naive_attention_fwd",
+    "attention_fwd", "attention_fwd_timed", "cast_f32_to_f16", "naive_attention_fwd",
     "CONFIGS", "Config",
 ]

@@ -27,6 +27,26 @@ def attention_fwd(Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray
                                        stream.handle if stream else None), "f3s_attention_fwd")
 
 
+def attention_fwd_timed(Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray,
+                        bsf: DeviceBSF, window_order: DeviceArray | None = None,
+                        masked: bool = True, H: int = 1, d: int = 64, scale: float = 1.0,
+                        reps: int = 10, stream: Stream | None = None) -> float:
+    """f3s_attention_fwd_timed: `reps` unplanned passes timed with HIP events
+    on the launch stream (the reference harness's timed launch,
+    tests/test_fused_3s_v2.cu:126-136); mean microseconds per pass."""
+    mask = bsf.tile_mask.ptr if (masked and bsf.tile_mask is not None) else None
+    if masked and mask is None:
+        raise ValueError("masked attention needs a BSF converted with masks")
+    us = C.c_float(0.0)
+    check(_lib.hip().f3s_attention_fwd_timed(Q.ptr, K.ptr, V.ptr, O.ptr, bsf.window_offsets.ptr,
+                                             bsf.block_col.ptr, mask,
+                                             window_order.ptr if window_order is not None else None,
+                                             bsf.W, bsf.n, d, H, scale,
+                                             stream.handle if stream else None, reps,
+                                             C.byref(us)), "f3s_attention_fwd_timed")
+    return float(us.value)
+
+
 class Plan:
     """f3s_plan: segments of heavy windows merged inside the launch."""
 

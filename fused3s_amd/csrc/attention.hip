@@ -1077,6 +1077,40 @@ f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_
     return F3S_OK;
 }
 
+f3s_status f3s_attention_fwd_timed(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                                   float* O, const int32_t* d_window_offsets,
+                                   const int32_t* d_block_col, const uint16_t* d_tile_mask,
+                                   const int32_t* d_window_order, int32_t W, int32_t n,
+                                   int32_t d, int32_t H, float scale, void* stream,
+                                   int32_t reps, float* us_out)
+{
+    F3S_REQUIRE(reps >= 1 && us_out, "f3s_attention_fwd_timed: reps >= 1 and us_out required");
+    F3S_TRY(check_attention_args(Q, K, V, O, n, d, H));
+    F3S_TRY(require_device());
+    hipStream_t st = as_stream(stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    F3S_HIP(hipEventCreate(&e0));
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return hip_fail(hipGetLastError(), "hipEventCreate", __FILE__, __LINE__);
+    }
+    f3s_status s = F3S_OK;
+    hipError_t he = hipEventRecord(e0, st);
+    for (int32_t i = 0; he == hipSuccess && s == F3S_OK && i < reps; ++i)
+        s = f3s_attention_fwd(Q, K, V, O, d_window_offsets, d_block_col, d_tile_mask,
+                              d_window_order, W, n, d, H, scale, stream);
+    float ms = 0.f;
+    if (he == hipSuccess && s == F3S_OK) he = hipEventRecord(e1, st);
+    if (he == hipSuccess && s == F3S_OK) he = hipEventSynchronize(e1);
+    if (he == hipSuccess && s == F3S_OK) he = hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (s != F3S_OK) return s;
+    if (he != hipSuccess) return hip_fail(he, "f3s_attention_fwd_timed", __FILE__, __LINE__);
+    *us_out = ms * 1000.0f / (float)reps;
+    return F3S_OK;
+}
+
 f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, const uint16_t* K,
                                      const uint16_t* V, float* O, const int32_t* d_block_col,
                                      const uint16_t* d_tile_mask, int32_t n, int32_t d, int32_t H,

@@ -123,6 +123,17 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
                              const int32_t* d_window_order, int32_t W, int32_t n,
                              int32_t d, int32_t H, float scale, void* stream);
 
+/* The timed launch of tests/test_fused_3s_v2.cu:126-136 (events recorded
+ * around the kernel on the launch stream): `reps` back-to-back calls of
+ * f3s_attention_fwd with the same arguments, timed with HIP events on
+ * `stream`; *us_out = mean microseconds per call.  Synchronises `stream`. */
+f3s_status f3s_attention_fwd_timed(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                                   float* O, const int32_t* d_window_offsets,
+                                   const int32_t* d_block_col, const uint16_t* d_tile_mask,
+                                   const int32_t* d_window_order, int32_t W, int32_t n,
+                                   int32_t d, int32_t H, float scale, void* stream,
+                                   int32_t reps, float* us_out);
+
 /* f3s_naive_baseline_kernel (baselines/gpu_baseline.cu:28-116): the naive
  * edge-exact comparator, one thread per node, fp32 Q/K/V/O [n][d], CSR
  * neighbours as stored (a duplicate entry counts twice, as in

@@ -56,6 +56,11 @@ def test_validation_happens_before_device_access():
                                    1, 16, 64, bad_h, 1.0, None) == 5
     # misaligned pointers are F3S_EINVAL
     assert h.f3s_attention_fwd(8, 16, 16, 16, 16, 16, None, None, 1, 16, 64, 1, 1.0, None) == 1
+    us = C.c_float()
+    assert h.f3s_attention_fwd_timed(None, None, None, None, None, None, None, None,
+                                     1, 16, 64, 1, 1.0, None, 0, C.byref(us)) == 1   # reps < 1
+    assert h.f3s_attention_fwd_timed(None, None, None, None, None, None, None, None,
+                                     1, 16, 64, 1, 1.0, None, 3, None) == 1          # no us_out
     T = C.c_int64()
     assert h.f3s_convert_csr_to_bsf(None, None, -1, 0, None, None, None, C.byref(T), None) == 1
     assert h.f3s_cast_f32_to_f16(None, None, -1, None) == 1

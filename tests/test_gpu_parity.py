@@ -365,6 +365,18 @@ def test_padding_slots_read_nothing(gpu, H):
             assert mabs <= ABS_TOL, f"H={H} masked={masked} planned={planned}: {mabs}"
 
 
+def test_attention_timed_entry(gpu):
+    rp, ci = random_csr(3000, 9, 33)
+    p = Problem(gpu, rp, ci, H=2, seed=33)
+    for masked in (True, False):
+        want = p.run(masked)
+        p.dO.fill_bytes(0xFF)
+        us = gpu.attention_fwd_timed(p.dQ, p.dK, p.dV, p.dO, p.bsf, masked=masked, H=2, reps=5)
+        assert us > 0.0
+        assert np.array_equal(p.dO.numpy().view(np.uint32), want.view(np.uint32))
+        log(f"  timed masked={masked}: {us:.1f} us per pass")
+
+
 def test_attention_rejects_bad_args(gpu):
     rp, ci = random_csr(40, 3, 1)
     p = Problem(gpu, rp, ci)
