@@ -322,6 +322,34 @@ def test_attention_closed_forms(gpu):
     rp1 = np.arange(n + 1, dtype=np.int32)
     p1 = Problem(gpu, rp1, np.arange(n, dtype=np.int32), seed=3)
     assert np.array_equal(p1.run(True)[:, 0], p1.Vf[:, 0])
+    # Q = K = V with identical rows: equal weights, so every row with a
+    # neighbour (masked) or with a tile (tile-dense) is that row
+    p2 = Problem(gpu, rp, ci, H=2, seed=4)
+    x = p2.Q[0].copy()
+    for a in (p2.Q, p2.K, p2.V):
+        a[:] = x
+    for d, a in zip((p2.dQ, p2.dK, p2.dV), (p2.Q, p2.K, p2.V)):
+        d.upload(a.view(np.uint16))
+    tiles = np.diff(p2.bsf.window_offsets.numpy())
+    for masked in (True, False):
+        has = deg > 0 if masked else np.repeat(tiles > 0, 16)[:n]
+        for planned in (False, True):
+            got = p2.run(masked, planned=planned, seg=4)
+            assert np.allclose(got[has], x.astype(np.float32), rtol=1e-6, atol=1e-7)
+            assert np.all(got[~has] == 0)
+    # tile-dense with K = 0: every row is the mean of V over its window's
+    # tile columns < n
+    p3 = Problem(gpu, rp, ci, seed=6)
+    p3.K[:] = 0
+    p3.dK.upload(p3.K.view(np.uint16))
+    hb = p3.host_bsf()
+    got = p3.run(False)[:, 0]
+    for w in range((n + 15) // 16):
+        b = hb.block_col_indices[hb.window_offsets[w]:hb.window_offsets[w + 1]]
+        cols = (b[:, None] * 16 + np.arange(16)).ravel()
+        cols = cols[cols < n]
+        want = p3.Vf[cols, 0].mean(axis=0) if len(cols) else np.zeros(64, np.float32)
+        assert np.allclose(got[16 * w:16 * w + 16], want, atol=1e-3)
 
 
 def test_attention_deterministic(gpu):

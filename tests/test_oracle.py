@@ -298,6 +298,12 @@ def test_masked_oracle_closed_forms_and_heads():
     O = orc.masked_attention(n, d, 1, f16_inputs((n, d), 5), f16_inputs((n, d), 6), V, rp1,
                              np.arange(n, dtype=np.int32))[:, 0]
     assert np.array_equal(O, V)
+    # Q = K = V with identical rows: every row with a neighbour is that row
+    x = f16_inputs((1, d), 11)[0]
+    same = np.tile(x, (n, 1))
+    O = orc.masked_attention(n, d, 1, same, same, same, rp, ci)[:, 0]
+    assert np.allclose(O[deg > 0], x, rtol=1e-6, atol=1e-7)
+    assert np.all(O[deg == 0] == 0)
     # H heads == H independent single-head problems
     H = 4
     Q, K, V4 = (f16_inputs((n, H, d), s) for s in (8, 9, 10))
