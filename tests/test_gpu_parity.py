@@ -405,6 +405,38 @@ def test_attention_timed_entry(gpu):
         log(f"  timed masked={masked}: {us:.1f} us per pass")
 
 
+def test_concurrent_streams_and_threads(gpu):
+    # Two host threads, each with its own stream, plan and output, run
+    # passes at the same time; each result equals a single-threaded run.
+    import threading
+    rp, ci = star_graph(6000, hubs=(2, 9))
+    p = Problem(gpu, rp, ci, H=2, normal=True, seed=35)
+    want = p.run(True, planned=True, seg=64, compiled=True)
+    outs, errs = {}, []
+
+    def worker(k):
+        try:
+            st = gpu.Stream()
+            plan = gpu.Plan(p.bsf, None, H=2, seg_tiles=64, stream=st)
+            plan.compile(st)
+            dO = gpu.DeviceArray((p.n, 2, 64), np.float32)
+            for _ in range(10):
+                plan.forward(p.dQ, p.dK, p.dV, dO, masked=True, stream=st)
+            st.synchronize()
+            outs[k] = dO.numpy()
+        except Exception as e:   # surfaced in the main thread
+            errs.append(e)
+
+    th = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join(timeout=120)
+    assert not errs, errs
+    for k in range(2):
+        assert np.array_equal(outs[k].view(np.uint32), want.view(np.uint32))
+
+
 def test_attention_rejects_bad_args(gpu):
     rp, ci = random_csr(40, 3, 1)
     p = Problem(gpu, rp, ci)
