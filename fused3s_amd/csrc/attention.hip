@@ -40,6 +40,7 @@
 // The k order inside a lane group is the same for A and B, so any consistent
 // assignment of k indices to (group, element) gives the same product; the
 // code relies only on that and on the row/column/C mapping.
+#include <algorithm>
 #include <math.h>
 #include <new>
 #include <stdio.h>
@@ -105,7 +106,36 @@ struct AttnParams {
     int64_t num_split;
     const int32_t* chunk_base;       // compiled plan: item i owns chunks [cb[i], cb[i+1])
     const uint32_t* columns;         // compiled plan: per chunk 32 row offsets, 32 row masks
+    int32_t team;                    // waves per window (1, or kTeamSmall / kTeamLarge)
 };
+
+// Small graphs: a team of waves in one workgroup shares each row window, each
+// wave taking an even share of the window's tiles (cut at tile pairs, the
+// tile-dense chunk), and the team merges its (m, l, O) states through LDS, so
+// the heaviest window no longer runs as one wave's serial chain and no merge
+// launch is needed.  Part k of a window's tiles [tb, te):
+__host__ __device__ __forceinline__ int32_t team_part(int32_t tb, int32_t te, int32_t k,
+                                                      int32_t team)
+{
+    const int64_t pairs = ((int64_t)te - tb + 1) / 2;
+    const int64_t a = tb + 2 * ((pairs * k) / team);
+    return (int32_t)(a < te ? a : te);
+}
+constexpr int kTeamSmall = 4;
+constexpr int kTeamLarge = 16;
+
+// Team size for W windows of H heads (measured on MI355X over graphs of
+// 170 to 62,500 windows): masked windows hold a few chunks each, so teams
+// of 4 pay while the windows leave most SIMDs idle; a tile-dense window is
+// ~15x the work, so teams of 16 pay on the smallest graphs and teams of 4
+// a little further.  1 = one wave per window or segment.
+static inline int32_t team_for(int64_t W, int32_t H, bool masked)
+{
+    const int64_t units = W * H;
+    if (masked) return units <= 1024 ? kTeamSmall : 1;
+    if (units <= 512) return kTeamLarge;
+    return units <= 2048 ? kTeamSmall : 1;
+}
 
 // Workgroup index -> logical block.  The dispatcher deals workgroups to the
 // 8 XCDs round-robin; with `xcd_contiguous` each XCD instead receives one
@@ -312,10 +342,11 @@ enum Mode : int {
 // chunk's gathers in flight per wave (double-buffered registers, 3 waves per
 // SIMD) measured no faster than one chunk per wave at 4-5 waves per SIMD, so
 // the simpler single-buffered loop is kept.
-template <int MODE, int WPG, bool WIDE>
+template <int MODE, int WPG, bool WIDE, int TEAM>
 __global__ void __launch_bounds__(kWave * WPG) __attribute__((amdgpu_waves_per_eu(4)))
 fused_attention_kernel(const AttnParams p)
 {
+    static_assert(TEAM == 1 || TEAM == WPG, "a team fills its workgroup");
     const int H = p.H;
     __shared__ WaveLds lds_all[WPG];
     const int wave = threadIdx.x / kWave;
@@ -325,10 +356,21 @@ fused_attention_kernel(const AttnParams p)
     WaveLds& L = lds_all[wave];
 
     const int32_t n = p.n;
-    // wave -> (item, head); the launch keeps num_items * H < 2^31
-    const uint32_t gw = (uint32_t)(logical_block(p.xcd_contiguous) * WPG + wave);
-    const int64_t item_idx = (int64_t)(gw / (uint32_t)H);
-    const int h = (int)(gw % (uint32_t)H);
+    // wave -> (item, head); the launch keeps num_items * H < 2^31.  A team's
+    // workgroup is one (window, head); its waves take the window's TEAM
+    // consecutive items, so every exit below is uniform over the workgroup
+    // (num_items is a multiple of TEAM).
+    int64_t item_idx;
+    int h;
+    if constexpr (TEAM == 1) {
+        const uint32_t gw = (uint32_t)(logical_block(p.xcd_contiguous) * WPG + wave);
+        item_idx = (int64_t)(gw / (uint32_t)H);
+        h = (int)(gw % (uint32_t)H);
+    } else {
+        const uint32_t gb = (uint32_t)logical_block(p.xcd_contiguous);
+        item_idx = (int64_t)(gb / (uint32_t)H) * TEAM + wave;
+        h = (int)(gb % (uint32_t)H);
+    }
     if (item_idx >= p.num_items) return;
 
     // ---- item decode (wave-uniform) ----
@@ -340,11 +382,17 @@ fused_attention_kernel(const AttnParams p)
         te = it.te;
         slot = it.slot;
     } else {
-        w = p.window_order ? p.window_order[item_idx] : (int32_t)item_idx;
+        const int64_t wi = item_idx / TEAM;
+        w = p.window_order ? p.window_order[wi] : (int32_t)wi;
         if (w < 0 || w >= p.W) return;
         const int32_t T = p.window_offsets[p.W];
         tb = max(0, min(p.window_offsets[w], T));
         te = max(tb, min(p.window_offsets[w + 1], T));
+        if constexpr (TEAM > 1) {
+            const int32_t a = team_part(tb, te, wave, TEAM), b = team_part(tb, te, wave + 1, TEAM);
+            tb = a;
+            te = b;
+        }
         slot = -1;
     }
     const int32_t nbc = (n + 15) >> 4;   // valid block columns
@@ -522,6 +570,41 @@ fused_attention_kernel(const AttnParams p)
         }
     }
 
+    if constexpr (TEAM > 1) {
+        // ---- team merge: waves 1.. publish (m, l, O^T) lane by lane in their
+        // own LDS area, wave 0 folds them in, in wave order (deterministic) ----
+        F3S_WAVE_LDS_SYNC();   // this wave's last reads of its stage are done
+        float* accs = reinterpret_cast<float*>(L.stage);   // [t][lane][4]: 4 KB of 4.5
+        if (wave != 0) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) *reinterpret_cast<f4*>(&accs[(t * kWave + lane) * 4]) = st.acc[t];
+            L.off[lane] = __float_as_uint(st.m);
+            L.rm[lane] = __float_as_uint(st.l);
+        }
+        __syncthreads();
+        if (wave != 0) return;
+        float M = st.m;
+#pragma unroll
+        for (int k = 1; k < TEAM; ++k) M = __builtin_fmaxf(M, __uint_as_float(lds_all[k].off[lane]));
+        if (M != -INFINITY) {   // else no part of the team attended row r: all zero
+            const float c0 = fast_exp2(st.m - M);   // 0 when this part is empty
+            st.l *= c0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) st.acc[t] *= c0;
+#pragma unroll
+            for (int k = 1; k < TEAM; ++k) {
+                const float mk = __uint_as_float(lds_all[k].off[lane]);
+                const float f = fast_exp2(mk - M);   // mk = -inf: 0
+                st.l += __uint_as_float(lds_all[k].rm[lane]) * f;
+                const float* ak = reinterpret_cast<const float*>(lds_all[k].stage);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    st.acc[t] += *reinterpret_cast<const f4*>(&ak[(t * kWave + lane) * 4]) * f;
+            }
+            st.m = M;
+        }
+    }
+
     // ---- epilogue ----
     const int32_t orow = w * 16 + r;
     float lrow = st.l + __shfl_xor(st.l, 16, kWave);
@@ -638,12 +721,18 @@ hipError_t warm_attention(hipStream_t s)
 // ----------------------------------------------------------------- planner
 
 __global__ void plan_count(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
-                           int32_t W, int32_t seg, int32_t* __restrict__ nitems,
+                           int32_t W, int32_t seg, int32_t team, int32_t* __restrict__ nitems,
                            int32_t* __restrict__ nslots, int32_t* __restrict__ nsplit)
 {
     const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
     if (L >= W) return;
     const int32_t w = order ? order[L] : L;
+    if (team > 1) {   // a team's items, merged in LDS: no partials
+        nitems[L] = team;
+        nslots[L] = 0;
+        nsplit[L] = 0;
+        return;
+    }
     int32_t ns = 1;
     if (w >= 0 && w < W) {
         const int32_t T = offs[W];
@@ -657,7 +746,8 @@ __global__ void plan_count(const int32_t* __restrict__ offs, const int32_t* __re
 }
 
 __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
-                          int32_t W, int32_t seg, const int64_t* __restrict__ item_base,
+                          int32_t W, int32_t seg, int32_t team,
+                          const int64_t* __restrict__ item_base,
                           const int64_t* __restrict__ slot_base,
                           const int64_t* __restrict__ split_base, Item* __restrict__ items,
                           SplitInfo* __restrict__ splits)
@@ -668,11 +758,17 @@ __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __res
     const int64_t ib = item_base[L];
     const int32_t ns = (int32_t)(item_base[L + 1] - ib);
     if (w < 0 || w >= W) {
-        items[ib] = Item{0, 0, 0, -1};   // empty item for an invalid order entry
+        for (int32_t k = 0; k < ns; ++k)
+            items[ib + k] = Item{0, 0, 0, -1};   // empty items for an invalid order entry
         return;
     }
     const int32_t T = offs[W];
     const int32_t tb = max(0, min(offs[w], T)), te = max(tb, min(offs[w + 1], T));
+    if (team > 1) {
+        for (int32_t k = 0; k < team; ++k)
+            items[ib + k] = Item{w, team_part(tb, te, k, team), team_part(tb, te, k + 1, team), -1};
+        return;
+    }
     if (ns == 1) {
         items[ib] = Item{w, tb, te, -1};
         return;
@@ -764,6 +860,7 @@ plan_columns(const Item* __restrict__ items, int64_t num_items,
 // into segments whose (m, l, O) partials a second launch merges.
 struct f3s_item_set {
     int32_t seg = 0;
+    int32_t team = 1;   // > 1: every window is one team of this many items, merged in LDS
     int64_t num_items = 0, num_split = 0, num_slots = 0;
     f3s::DeviceBuffer items, splits, partials;
 };
@@ -774,9 +871,11 @@ struct f3s_plan {
     int64_t T = 0;
     // Masked passes (compiled lists or tile expansion) run `masked`.  A
     // tile-dense chunk costs two whole tiles, about 15x a masked chunk per
-    // tile on sparse graphs, so tile-dense passes run `dense`, cut finer;
-    // dense.seg == 0 means they share `masked` (an explicit segment size).
+    // tile on sparse graphs, so automatic plans give tile-dense passes their
+    // own item set, `dense`, cut finer; without it (has_dense == false, e.g.
+    // an explicit segment size) they share `masked`.
     f3s_item_set masked, dense;
+    bool has_dense = false;
     // compiled column lists (f3s_plan_compile) and the structure they describe
     f3s::DeviceBuffer chunk_base, columns;
     const int32_t* compiled_block_col = nullptr;
@@ -789,10 +888,11 @@ namespace f3s {
 
 static f3s_status build_items(f3s_item_set& set, const int32_t* d_window_offsets,
                               const int32_t* d_window_order, int32_t W, int32_t H, int64_t seg,
-                              hipStream_t st)
+                              int32_t team, hipStream_t st)
 {
     if (seg > INT32_MAX) seg = INT32_MAX;
     set.seg = (int32_t)seg;
+    set.team = team;
     DeviceBuffer cnt_items, cnt_slots, cnt_split, base_items, base_slots, base_split, tmp;
     f3s_status s;
     if ((s = cnt_items.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
@@ -811,7 +911,7 @@ static f3s_status build_items(f3s_item_set& set, const int32_t* d_window_offsets
     auto* bp = reinterpret_cast<int64_t*>(base_split.ptr);
     if (W > 0) {
         hipLaunchKernelGGL(plan_count, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
-                           d_window_offsets, d_window_order, W, set.seg, ci, cs, cp);
+                           d_window_offsets, d_window_order, W, set.seg, team, ci, cs, cp);
         F3S_HIP(hipGetLastError());
     }
     auto* tp = reinterpret_cast<int64_t*>(tmp.ptr);
@@ -832,7 +932,7 @@ static f3s_status build_items(f3s_item_set& set, const int32_t* d_window_offsets
                                  (size_t)(set.num_slots + 1)));
     if (W > 0) {
         hipLaunchKernelGGL(plan_fill, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
-                           d_window_offsets, d_window_order, W, set.seg, bi, bs, bp,
+                           d_window_offsets, d_window_order, W, set.seg, team, bi, bs, bp,
                            reinterpret_cast<Item*>(set.items.ptr),
                            reinterpret_cast<SplitInfo*>(set.splits.ptr));
         F3S_HIP(hipGetLastError());
@@ -869,12 +969,27 @@ static f3s_status check_attention_args(const void* Q, const void* K, const void*
 template <int MODE, bool WIDE>
 static void launch_mw(const AttnParams& p, int64_t waves, hipStream_t st)
 {
+    if constexpr (!WIDE) {
+        // teams (small graphs; never wide): one workgroup per (window, head)
+        if (p.team == kTeamLarge) {
+            hipLaunchKernelGGL((fused_attention_kernel<MODE, kTeamLarge, false, kTeamLarge>),
+                               dim3((unsigned)(waves / kTeamLarge)), dim3(kTeamLarge * kWave), 0,
+                               st, p);
+            return;
+        }
+        if (p.team == kTeamSmall) {
+            hipLaunchKernelGGL((fused_attention_kernel<MODE, kTeamSmall, false, kTeamSmall>),
+                               dim3((unsigned)(waves / kTeamSmall)), dim3(kTeamSmall * kWave), 0,
+                               st, p);
+            return;
+        }
+    }
     // Small launches use one-wave workgroups so they spread over all CUs.
     if (waves < 4 * 256 * 2) {
-        hipLaunchKernelGGL((fused_attention_kernel<MODE, 1, WIDE>), dim3((unsigned)waves),
+        hipLaunchKernelGGL((fused_attention_kernel<MODE, 1, WIDE, 1>), dim3((unsigned)waves),
                            dim3(kWave), 0, st, p);
     } else {
-        hipLaunchKernelGGL((fused_attention_kernel<MODE, 4, WIDE>),
+        hipLaunchKernelGGL((fused_attention_kernel<MODE, 4, WIDE, 1>),
                            dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
     }
     if (p.num_split > 0)
@@ -901,6 +1016,11 @@ static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
     // narrow launches range-check buffer loads against the tensor size;
     // wide ones never use the buffer descriptors
     p.feat_bytes = wide_features(p.n, H) ? 0u : (uint32_t)((int64_t)p.n * H * kRowBytes);
+    if (p.team > 1) {
+        F3S_REQUIRE((p.team == kTeamSmall || p.team == kTeamLarge) && p.num_items % p.team == 0 &&
+                        p.num_split == 0 && !wide_features(p.n, H),
+                    "attention: invalid team launch");
+    }
     if (!p.tile_mask)
         launch_m<kModeDense>(p, waves, st);
     else if (p.chunk_base)
@@ -939,7 +1059,8 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
     p.block_col = d_block_col;
     p.tile_mask = d_tile_mask;
     p.window_order = d_window_order;
-    p.num_items = W;
+    p.team = team_for(W, H, d_tile_mask != nullptr);
+    p.num_items = (int64_t)W * p.team;
     p.W = W;
     p.n = n;
     p.xcd_contiguous = d_window_order == nullptr;
@@ -974,22 +1095,26 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     p->H = H;
     p->natural_order = d_window_order == nullptr;
     p->T = T32;
-    // Automatic segment sizes: enough segments that the heaviest item is a
-    // small fraction of one wave slot's share of the pass (5,120 wave slots).
-    // Masked passes: small graphs are not split, since a merge launch costs
-    // more than the serial tail it removes; tile-dense passes: a segment is at
-    // most a tenth of a slot's share, and at least 16 tiles.
+    // Automatic plans.  A window is cut into segments only when it is well
+    // above the mean window (4x masked, 2x tile-dense: cutting every window
+    // of a uniform graph just adds merge traffic) and a large share of one
+    // wave slot's part of the pass (5,120 slots; a tenth of it for
+    // tile-dense).  Graphs whose windows leave most SIMDs idle run teams
+    // instead (team_for), as the unplanned launch does.
     int64_t seg_m = seg_tiles, seg_d = 0;
-    if (seg_m == 0) {
-        seg_m = ceil_div(p->T * H, 8192);
-        if (seg_m < 256) seg_m = 256;
-        seg_d = ceil_div(p->T * H, 51200);
-        if (seg_d < 16) seg_d = 16;
-        if (seg_d >= seg_m) seg_d = 0;
+    int32_t team_m = 1, team_d = 1;
+    if (seg_tiles == 0) {
+        const int64_t mean = W > 0 ? ceil_div(p->T, W) : 0;
+        team_m = team_for(W, H, true);
+        team_d = team_for(W, H, false);
+        seg_m = std::max<int64_t>({256, 4 * mean, ceil_div(p->T * H, 8192)});
+        seg_d = std::max<int64_t>({16, 2 * mean, ceil_div(p->T * H, 51200)});
+        p->has_dense = team_d != team_m || (team_d == 1 && seg_d != seg_m);
     }
-    f3s_status s = build_items(p->masked, d_window_offsets, d_window_order, W, H, seg_m, st);
-    if (s == F3S_OK && seg_d > 0)
-        s = build_items(p->dense, d_window_offsets, d_window_order, W, H, seg_d, st);
+    f3s_status s =
+        build_items(p->masked, d_window_offsets, d_window_order, W, H, seg_m, team_m, st);
+    if (s == F3S_OK && p->has_dense)
+        s = build_items(p->dense, d_window_offsets, d_window_order, W, H, seg_d, team_d, st);
     if (s != F3S_OK) {
         delete p;
         return s;
@@ -1134,7 +1259,7 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
     p.block_col = d_block_col;
     p.tile_mask = d_tile_mask;
     // tile-dense passes run the finer item set when the plan has one
-    const f3s_item_set& set = (!d_tile_mask && plan->dense.seg > 0) ? plan->dense : plan->masked;
+    const f3s_item_set& set = (!d_tile_mask && plan->has_dense) ? plan->dense : plan->masked;
     p.items = reinterpret_cast<const Item*>(set.items.ptr);
     p.num_items = set.num_items;
     p.W = plan->W;
@@ -1143,6 +1268,7 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
     p.partials = reinterpret_cast<float*>(set.partials.ptr);
     p.splits = reinterpret_cast<const SplitInfo*>(set.splits.ptr);
     p.num_split = set.num_split;
+    p.team = set.team;
     if (d_tile_mask && d_tile_mask == plan->compiled_tile_mask &&
         d_block_col == plan->compiled_block_col && n == plan->compiled_n) {
         p.chunk_base = reinterpret_cast<const int32_t*>(plan->chunk_base.ptr);

@@ -116,7 +116,9 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * attended column get 0.  Requires d == 64 and 1 <= H <= 64 heads in
  * node-major [n][H][64] layout, of any size (tensors past ~4 GiB are read
  * with 64-bit addresses); scale = 1 reproduces the reference (which has no
- * scaling, and one head). */
+ * scaling, and one head).  Small graphs (W*H <= 2048) run each window on a
+ * team of 16 (W*H <= 512) or 4 waves of one workgroup, each wave taking an
+ * even share of the window's tiles, merged in LDS in a fixed order. */
 f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                              float* O, const int32_t* d_window_offsets,
                              const int32_t* d_block_col, const uint16_t* d_tile_mask,
@@ -145,10 +147,11 @@ f3s_status f3s_naive_attention_fwd(const float* Q, const float* K, const float* 
 
 /* Planned execution (no reference counterpart; the reference relies on the
  * window sort alone, include/utils.cuh:48-59).  A plan splits windows with
- * more than `seg_tiles` tiles (0 = automatic: none on small graphs) into
- * segments processed by separate waves; a second, small launch merges each
- * split window's segments in a fixed order (deterministic), so hub windows do
- * not serialise.  Windows run in d_window_order (the reference's descending
+ * more than `seg_tiles` tiles into segments processed by separate waves; a
+ * second, small launch merges each split window's segments in a fixed order
+ * (deterministic), so hub windows do not serialise.  seg_tiles = 0 chooses
+ * automatically: on small graphs (W*H <= 2048) the teams of f3s_attention_fwd
+ * (same items, same bits), else segment sizes from T*H.  Windows run in d_window_order (the reference's descending
  * sort) or, when it is NULL, in natural order with consecutive windows kept
  * on one XCD (for community-ordered graphs).  Build once per graph; reuse for
  * every forward pass; one plan must not serve two overlapping calls (it owns

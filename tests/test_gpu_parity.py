@@ -289,6 +289,41 @@ def test_attention_random_heads(gpu, H, n, deg, seed):
                                     f"compiled={compiled}")
 
 
+@pytest.mark.parametrize("case,H,team_m,team_d", [("random", 1, 4, 16), ("random", 4, 4, 4),
+                                                 ("random", 8, 1, 4), ("random", 16, 1, 1),
+                                                 ("star", 1, 4, 16), ("star", 3, 4, 4)])
+def test_attention_teams(gpu, case, H, team_m, team_d):
+    # Small graphs run each window on a team of waves that merge in LDS:
+    # masked, 4 waves while W*H <= 1024; tile-dense, 16 while W*H <= 512 and
+    # 4 up to 2048.  The unplanned launch and an automatic plan make the same
+    # items (same bits, with or without compiled lists, in any window order);
+    # both meet the oracle.
+    rp, ci = random_csr(3000, 10, 41) if case == "random" else star_graph(5000, hubs=(0, 7))
+    p = Problem(gpu, rp, ci, H=H, normal=True, seed=41)
+    W = (p.n + 15) // 16
+    plan = gpu.Plan(p.bsf, None, H=H)
+    if team_m > 1:   # plan_info describes the masked item set
+        assert plan.num_items == W * team_m and plan.num_split == 0
+    else:
+        assert plan.num_items < W * 4
+    order = gpu.window_order_device(p.bsf)
+    for masked in (True, False):
+        team = team_m if masked else team_d
+        want = p.oracle(masked, scale=0.125)
+        base = p.run(masked, scale=0.125)
+        assert_close(base, want, f"{case} H={H} team={team} masked={masked}")
+        variants = [("planned", dict(planned=True)), ("ordered", dict(order=order)),
+                    ("planned+ordered", dict(planned=True, order=order))]
+        if masked:
+            variants.append(("compiled", dict(planned=True, compiled=True)))
+        for what, kw in variants:
+            got = p.run(masked, scale=0.125, **kw)
+            if team > 1:
+                assert np.array_equal(got.view(np.uint32), base.view(np.uint32)), what
+            else:
+                assert_close(got, want, f"{case} H={H} masked={masked} {what}")
+
+
 def test_attention_hub_split_merge(gpu):
     rp, ci = star_graph(20000, hubs=(0, 3, 17))
     p = Problem(gpu, rp, ci, H=1, normal=True, seed=9)
