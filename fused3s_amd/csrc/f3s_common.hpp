@@ -46,6 +46,9 @@ struct DeviceBuffer {
     size_t bytes = 0;
     f3s_status reserve(size_t want);
     void release();
+    DeviceBuffer() = default;
+    DeviceBuffer(const DeviceBuffer&) = delete;              // owns its allocation
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
     ~DeviceBuffer() { release(); }
 };
 
