@@ -694,8 +694,7 @@ static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
         launch_mw<MODE, false>(p, waves, st);
 }
 
-static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st,
-                         const f3s_plan* panels = nullptr)
+static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
 {
     if (p.num_items <= 0) return F3S_OK;
     const int64_t waves = p.num_items * H;
@@ -710,9 +709,7 @@ static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st,
                         p.num_split == 0 && !wide_features(p.n, H),
                     "attention: invalid team launch");
     }
-    if (panels)
-        panel_launch(panels, p, st);
-    else if (!p.tile_mask)
+    if (!p.tile_mask)
         launch_m<kModeDense>(p, waves, st);
     else if (p.chunk_base)
         launch_m<kModeList>(p, waves, st);
@@ -828,17 +825,6 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     plan->compiled_tile_mask = nullptr;
     plan->compiled_block_col = nullptr;
     plan->compiled_n = -1;
-    // community-ordered graphs: panels, when they pay, replace the lists
-    F3S_TRY(panel_compile_plan(plan, d_block_col, d_tile_mask, n, st));
-    if (plan->panels) {
-        plan->columns.release();
-        plan->chunk_base.release();
-        plan->num_chunks = 0;
-        plan->compiled_tile_mask = d_tile_mask;
-        plan->compiled_block_col = d_block_col;
-        plan->compiled_n = n;
-        return F3S_OK;
-    }
     const int64_t ni = plan->masked.num_items;
     DeviceBuffer counts, tmp;
     F3S_TRY(counts.reserve(sizeof(int32_t) * (size_t)(ni + 1)));
@@ -901,16 +887,6 @@ f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_
     if (num_split_windows) *num_split_windows = plan->masked.num_split;
     if (T) *T = plan->T;
     if (seg_tiles) *seg_tiles = plan->masked.seg;
-    return F3S_OK;
-}
-
-f3s_status f3s_plan_panels(const f3s_plan* plan, int64_t* num_panels, int64_t* rows_gathered,
-                           int64_t* rows_fetched)
-{
-    F3S_REQUIRE(plan != nullptr, "f3s_plan_panels: NULL plan");
-    if (num_panels) *num_panels = plan->panels ? plan->num_panels : 0;
-    if (rows_gathered) *rows_gathered = plan->pn_rows_gathered;
-    if (rows_fetched) *rows_fetched = plan->pn_rows_fetched;
     return F3S_OK;
 }
 
@@ -983,7 +959,6 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
     p.team = set.team;
     if (d_tile_mask && d_tile_mask == plan->compiled_tile_mask &&
         d_block_col == plan->compiled_block_col && n == plan->compiled_n) {
-        if (plan->panels) return launch(p, H, scale, as_stream(stream), plan);
         p.chunk_base = reinterpret_cast<const int32_t*>(plan->chunk_base.ptr);
         p.columns = reinterpret_cast<const uint32_t*>(plan->columns.ptr);
     }

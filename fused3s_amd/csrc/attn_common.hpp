@@ -1,7 +1,6 @@
-// attn_common.hpp -- building blocks shared by the fused attention passes
-// (attention.hip: one wave or one team per row window; panel.hip: row windows
-// sharing K/V rows through LDS): operand types and layouts, row references,
-// the per-row online-softmax state and the 32-column MFMA chunk step.
+// attn_common.hpp -- building blocks of the fused attention kernels
+// (attention.hip): operand types and layouts, row references, the per-row
+// online-softmax state and the 32-column MFMA chunk step.
 #pragma once
 
 #include <math.h>

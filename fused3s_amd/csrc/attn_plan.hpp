@@ -1,5 +1,5 @@
 // attn_plan.hpp -- the plan object behind f3s_plan_create / f3s_plan_compile
-// (work items, segment partials, compiled column lists, panels).
+// (work items, segment partials, compiled column lists).
 #pragma once
 
 #include "attn_common.hpp"
@@ -30,16 +30,4 @@ struct f3s_plan {
     const uint16_t* compiled_tile_mask = nullptr;
     int32_t compiled_n = -1;
     int64_t num_chunks = 0;
-    // panels (panel.hip): compiled instead of the column lists when they
-    // pay; masked passes with the compiled structure then run the panel pass
-    bool panels = false;
-    int64_t num_panels = 0, num_panel_chunks = 0;
-    int64_t pn_rows_gathered = 0, pn_rows_fetched = 0;   // K/V row fetches without / with
-    f3s::DeviceBuffer pn_nslots, pn_slot_base, pn_slot_refs, pn_chunk_base, pn_records;
 };
-
-namespace f3s {
-f3s_status panel_compile_plan(f3s_plan* plan, const int32_t* d_block_col,
-                              const uint16_t* d_tile_mask, int32_t n, hipStream_t st);
-void panel_launch(const f3s_plan* plan, const AttnParams& p, hipStream_t st);
-}  // namespace f3s

@@ -79,8 +79,3 @@ struct DeviceBuffer {
 // before any issued after, and the compiler may not move memory operations
 // across it.  Sufficient for LDS shared between the lanes of one wave.
 #define F3S_WAVE_LDS_SYNC() asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory")
-
-// Waits until every vector-memory load this wave issued has completed,
-// including loads that write LDS directly (buffer_load ... lds); the
-// compiler may not move memory operations across it.
-#define F3S_VMEM_SYNC() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")

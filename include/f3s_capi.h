@@ -172,17 +172,6 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
                             const uint16_t* d_tile_mask, int32_t n, void* stream);
 f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_split_windows,
                          int64_t* T, int32_t* seg_tiles);
-/* Panels (no reference counterpart).  On community-ordered graphs (plans
- * made without a window order, no split windows) f3s_plan_compile groups 16
- * consecutive windows into a panel whose K/V rows attended by two or more of
- * its windows are loaded into LDS once per pass and shared, when that cuts
- * the K/V row fetches by at least 1.3x; later masked passes with the
- * compiled structure run one 16-wave workgroup per (panel, head).
- * *num_panels = 0 when the compiled plan does not use them.  rows_gathered /
- * rows_fetched: K/V row fetches per head without / with panels, from the last
- * f3s_plan_compile (0 before it). */
-f3s_status f3s_plan_panels(const f3s_plan* plan, int64_t* num_panels, int64_t* rows_gathered,
-                           int64_t* rows_fetched);
 f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q,
                                      const uint16_t* K, const uint16_t* V, float* O,
                                      const int32_t* d_block_col, const uint16_t* d_tile_mask,
