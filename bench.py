@@ -116,9 +116,8 @@ def main() -> int:
     ap.add_argument("--seg", type=int, default=0,
                     help="plan segment size in tiles (0 = automatic)")
     ap.add_argument("--no-compile", action="store_true",
-                    help="skip f3s_plan_compile: masked passes expand tiles on every pass "
-                         "instead of using compiled column lists, and tile-dense passes on "
-                         "community-ordered graphs gather every tile instead of using panels")
+                    help="masked passes expand tiles on every pass instead of using the "
+                         "plan's compiled column lists")
     ap.add_argument("--heads", type=int, default=0,
                     help="override the configuration's head count (1 to 64); the line is "
                          "then not the configuration's own workload")
@@ -187,7 +186,7 @@ def main() -> int:
     order = f3s.window_order_device(bsf, stream) if use_sorted else None
     ev0.record(stream)
     plan = f3s.Plan(bsf, order, H=H, seg_tiles=args.seg, stream=stream)
-    if not args.no_compile:   # masked lists; tile-dense panels where they pay
+    if masked and not args.no_compile:
         plan.compile(stream)
     ev1.record(stream)
     plan_ms = ev0.elapsed_ms(ev1)
@@ -257,8 +256,7 @@ def main() -> int:
         "converter_us": conv_ms * 1e3,
         "converter_end_to_end_us": conv_e2e_ms * 1e3,
         "plan_us": plan_ms * 1e3,
-        "plan_compiled": not args.no_compile,
-        "tile_dense_panels": plan.panel_info()[0] if not masked else None,
+        "plan_compiled": bool(masked and not args.no_compile),
         "device": f3s.device_name(),
     }
     if not args.no_cpu_baseline:

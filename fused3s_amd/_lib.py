@@ -56,7 +56,6 @@ HIP_API = {
     "f3s_plan_destroy": (c_i32, [c_vp]),
     "f3s_plan_compile": (c_i32, [c_vp, c_vp, c_vp, c_i32, c_vp]),
     "f3s_plan_info": (c_i32, [c_vp, P_i64, P_i64, P_i64, P_i32]),
-    "f3s_plan_panels": (c_i32, [c_vp, P_i64, P_i64, P_i64]),
     "f3s_attention_fwd_planned": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                           c_i32, c_i32, c_i32, c_f32, c_vp]),
 }

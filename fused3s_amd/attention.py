@@ -75,14 +75,6 @@ class Plan:
                                           bsf.n, stream.handle if stream else None),
               "f3s_plan_compile")
 
-    def panel_info(self) -> tuple[int, int, int]:
-        """f3s_plan_panels: (tile-dense panels in use, K/V row fetches per
-        head of a tile-dense pass without panels, with them)."""
-        np_, g, f = C.c_int64(), C.c_int64(), C.c_int64()
-        check(_lib.hip().f3s_plan_panels(self.handle, C.byref(np_), C.byref(g), C.byref(f)),
-              "f3s_plan_panels")
-        return np_.value, g.value, f.value
-
     def forward(self, Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray,
                 masked: bool = True, d: int = 64, scale: float = 1.0,
                 stream: Stream | None = None) -> None:

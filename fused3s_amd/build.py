@@ -23,8 +23,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
-HIP_SOURCES = ["runtime.hip", "convert.hip", "attention.hip", "panel.hip", "bsf_util.hip",
-               "naive.hip"]
+HIP_SOURCES = ["runtime.hip", "convert.hip", "attention.hip", "bsf_util.hip", "naive.hip"]
 HOST_SOURCES = ["host/gen.cpp", "host/graph.cpp", "host/graph_file.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -332,26 +332,6 @@ fused_attention_kernel(const AttnParams p)
     const int32_t orow = w * 16 + r;
     float lrow = st.l + __shfl_xor(st.l, 16, kWave);
     lrow += __shfl_xor(lrow, 32, kWave);
-    if constexpr (MODE == kModeDense && TEAM == 1) {
-        if (p.prior && slot < 0) {   // fold in the window's staged-tile partial (panels)
-            const float* part = p.prior + ((int64_t)w * H + h) * kPartialFloats;
-            const float pm = part[16 * kD + r], pl = part[16 * kD + 16 + r];
-            const float M = __builtin_fmaxf(st.m, pm);
-            if (M != -INFINITY) {   // else neither part attended row r: all zero
-                const float fa = fast_exp2(st.m - M), fb = fast_exp2(pm - M);
-                lrow = lrow * fa + pl * fb;
-                const float* src = part + r * kD + 16 * g;
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const float4 a = *reinterpret_cast<const float4*>(src + 4 * v);
-                    st.acc[0][v] = st.acc[0][v] * fa + a.x * fb;
-                    st.acc[1][v] = st.acc[1][v] * fa + a.y * fb;
-                    st.acc[2][v] = st.acc[2][v] * fa + a.z * fb;
-                    st.acc[3][v] = st.acc[3][v] * fa + a.w * fb;
-                }
-            }
-        }
-    }
     if (slot < 0) {
         const float inv = lrow > 0.f ? 1.0f / lrow : 0.f;
         if (orow < n) {
@@ -714,8 +694,7 @@ static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
         launch_mw<MODE, false>(p, waves, st);
 }
 
-static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st,
-                         const f3s_plan* panels = nullptr)
+static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
 {
     if (p.num_items <= 0) return F3S_OK;
     const int64_t waves = p.num_items * H;
@@ -730,15 +709,7 @@ static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st,
                         p.num_split == 0 && !wide_features(p.n, H),
                     "attention: invalid team launch");
     }
-    if (panels) {
-        // staged tiles (partials), then each window's residual tiles, whose
-        // pass folds the partial in
-        panel_launch(panels, p, st);
-        p.items = reinterpret_cast<const Item*>(panels->pn_res_items.ptr);
-        p.block_col = reinterpret_cast<const int32_t*>(panels->pn_res_block_col.ptr);
-        p.prior = reinterpret_cast<const float*>(panels->pn_partials.ptr);
-        launch_m<kModeDense>(p, waves, st);
-    } else if (!p.tile_mask)
+    if (!p.tile_mask)
         launch_m<kModeDense>(p, waves, st);
     else if (p.chunk_base)
         launch_m<kModeList>(p, waves, st);
@@ -854,7 +825,6 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     plan->compiled_tile_mask = nullptr;
     plan->compiled_block_col = nullptr;
     plan->compiled_n = -1;
-    plan->panels = false;
     const int64_t ni = plan->masked.num_items;
     DeviceBuffer counts, tmp;
     F3S_TRY(counts.reserve(sizeof(int32_t) * (size_t)(ni + 1)));
@@ -897,8 +867,6 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     F3S_HIP(hipGetLastError());
     F3S_HIP(hipStreamSynchronize(st));
     plan->num_chunks = total;
-    // community-ordered graphs: tile-dense panels, when they pay
-    F3S_TRY(panel_compile_plan(plan, d_block_col, n, st));
     plan->compiled_tile_mask = d_tile_mask;
     plan->compiled_block_col = d_block_col;
     plan->compiled_n = n;
@@ -919,16 +887,6 @@ f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_
     if (num_split_windows) *num_split_windows = plan->masked.num_split;
     if (T) *T = plan->T;
     if (seg_tiles) *seg_tiles = plan->masked.seg;
-    return F3S_OK;
-}
-
-f3s_status f3s_plan_panels(const f3s_plan* plan, int64_t* num_panels, int64_t* rows_gathered,
-                           int64_t* rows_fetched)
-{
-    F3S_REQUIRE(plan != nullptr, "f3s_plan_panels: NULL plan");
-    if (num_panels) *num_panels = plan->panels ? plan->num_panels : 0;
-    if (rows_gathered) *rows_gathered = plan->pn_rows_gathered;
-    if (rows_fetched) *rows_fetched = plan->pn_rows_fetched;
     return F3S_OK;
 }
 
@@ -999,16 +957,6 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
     p.splits = reinterpret_cast<const SplitInfo*>(set.splits.ptr);
     p.num_split = set.num_split;
     p.team = set.team;
-    if (!d_tile_mask && plan->panels && d_block_col == plan->compiled_block_col &&
-        n == plan->compiled_n) {
-        // tile-dense panels: one residual item per window, no split windows
-        p.num_items = plan->W;
-        p.partials = nullptr;
-        p.splits = nullptr;
-        p.num_split = 0;
-        p.team = 1;
-        return launch(p, H, scale, as_stream(stream), plan);
-    }
     if (d_tile_mask && d_tile_mask == plan->compiled_tile_mask &&
         d_block_col == plan->compiled_block_col && n == plan->compiled_n) {
         p.chunk_base = reinterpret_cast<const int32_t*>(plan->chunk_base.ptr);

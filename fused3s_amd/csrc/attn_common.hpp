@@ -67,8 +67,6 @@ struct AttnParams {
     const int32_t* chunk_base;       // compiled plan: item i owns chunks [cb[i], cb[i+1])
     const uint32_t* columns;         // compiled plan: per chunk 32 row offsets, 32 row masks
     int32_t team;                    // waves per window (1, or kTeamSmall / kTeamLarge)
-    const float* prior;              // tile-dense, whole windows: partial (O, m, l) per
-                                     // (window, head) folded in before O is written
 };
 
 // Small graphs: a team of waves in one workgroup shares each row window, each

@@ -1,5 +1,5 @@
 // attn_plan.hpp -- the plan object behind f3s_plan_create / f3s_plan_compile
-// (work items, segment partials, compiled column lists, tile-dense panels).
+// (work items, segment partials, compiled column lists).
 #pragma once
 
 #include "attn_common.hpp"
@@ -30,18 +30,4 @@ struct f3s_plan {
     const uint16_t* compiled_tile_mask = nullptr;
     int32_t compiled_n = -1;
     int64_t num_chunks = 0;
-    // tile-dense panels (panel.hip), built by f3s_plan_compile when they pay:
-    // staged tiles per panel, the residual tiles per window, and the staged
-    // tiles' partials the residual pass folds in
-    bool panels = false;
-    int64_t num_panels = 0, num_panel_chunks = 0;
-    int64_t pn_rows_gathered = 0, pn_rows_fetched = 0;   // K/V row fetches without / with
-    f3s::DeviceBuffer pn_nslots, pn_slot_base, pn_slot_refs, pn_chunk_base, pn_records;
-    f3s::DeviceBuffer pn_res_block_col, pn_res_items, pn_partials;
 };
-
-namespace f3s {
-f3s_status panel_compile_plan(f3s_plan* plan, const int32_t* d_block_col, int32_t n,
-                              hipStream_t st);
-void panel_launch(const f3s_plan* plan, const AttnParams& p, hipStream_t st);
-}  // namespace f3s

@@ -172,19 +172,6 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
                             const uint16_t* d_tile_mask, int32_t n, void* stream);
 f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_split_windows,
                          int64_t* T, int32_t* seg_tiles);
-/* Tile-dense panels (no reference counterpart).  On community-ordered graphs
- * (plans made without a window order, no split windows) f3s_plan_compile
- * groups 16 consecutive windows into a panel: the block columns active in two
- * or more of its windows have their K/V rows loaded into LDS once per pass and
- * shared, and each window's other tiles run through the gathered pass, which
- * folds the shared part in.  Kept when it cuts the K/V row fetches at least
- * 1.5x; later tile-dense calls of f3s_attention_fwd_planned with the compiled
- * block_col and n then use it (masked calls are unaffected).  *num_panels = 0
- * when the plan does not use panels; rows_gathered / rows_fetched: K/V row
- * fetches per head of a tile-dense pass without / with panels, from the last
- * f3s_plan_compile (0 before it). */
-f3s_status f3s_plan_panels(const f3s_plan* plan, int64_t* num_panels, int64_t* rows_gathered,
-                           int64_t* rows_fetched);
 f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q,
                                      const uint16_t* K, const uint16_t* V, float* O,
                                      const int32_t* d_block_col, const uint16_t* d_tile_mask,

@@ -64,7 +64,6 @@ def test_validation_happens_before_device_access():
     T = C.c_int64()
     assert h.f3s_convert_csr_to_bsf(None, None, -1, 0, None, None, None, C.byref(T), None) == 1
     assert h.f3s_cast_f32_to_f16(None, None, -1, None) == 1
-    assert h.f3s_plan_panels(None, None, None, None) == 1
 
 
 def test_no_device_is_reported_not_faked():
