@@ -104,6 +104,7 @@ fused_attention_kernel(const AttnParams p)
         tb = it.tb;
         te = it.te;
         slot = it.slot;
+        if (w < 0 || w >= p.W) return;   // an invalid order entry (a whole team's items)
     } else {
         const int64_t wi = item_idx / TEAM;
         w = p.window_order ? p.window_order[wi] : (int32_t)wi;
@@ -482,7 +483,7 @@ __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __res
     const int32_t ns = (int32_t)(item_base[L + 1] - ib);
     if (w < 0 || w >= W) {
         for (int32_t k = 0; k < ns; ++k)
-            items[ib + k] = Item{0, 0, 0, -1};   // empty items for an invalid order entry
+            items[ib + k] = Item{-1, 0, 0, -1};   // no window: the pass skips these
         return;
     }
     const int32_t T = offs[W];

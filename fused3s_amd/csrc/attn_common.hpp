@@ -28,7 +28,8 @@ constexpr int32_t kBufferFlags = 0x00020000;
 // Row-mask layout in the ring: bit k = row 2k, bit 16 + k = row 2k + 1.
 
 struct Item {
-    int32_t w, tb, te, slot;       // slot < 0: whole window, write O directly
+    int32_t w, tb, te, slot;       // slot < 0: whole window, write O directly;
+                                   // w < 0: no window (an invalid order entry), skipped
 };
 
 struct SplitInfo {

@@ -472,6 +472,32 @@ def test_concurrent_streams_and_threads(gpu):
         assert np.array_equal(outs[k].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("H", [1, 16])
+def test_window_order_with_invalid_entries(gpu, H):
+    # A caller's window order may name invalid windows (< 0 or >= W): they
+    # are skipped, the windows it does not name are left unwritten, and the
+    # named ones are exact -- with teams (H = 1) and without (H = 16), planned
+    # or not.
+    rp, ci = random_csr(3000, 8, 51)
+    p = Problem(gpu, rp, ci, H=H, normal=True, seed=51)
+    W = (p.n + 15) // 16
+    order = rng(52).permutation(W).astype(np.int32)
+    dropped = order[::5].copy()
+    order[::5] = np.where(np.arange(len(dropped)) % 2 == 0, -1, W + 3)
+    dorder = gpu.DeviceArray.from_numpy(order)
+    named = np.ones(W, bool)
+    named[dropped] = False
+    rows = np.repeat(named, 16)[:p.n]
+    for masked in (True, False):
+        want = p.oracle(masked, scale=0.125)
+        for planned, compiled in ((False, False), (True, False), (True, True)):
+            got = p.run(masked, planned=planned, order=dorder, scale=0.125,
+                        compiled=compiled and masked)
+            what = f"invalid order H={H} masked={masked} planned={planned} compiled={compiled}"
+            assert np.all(np.isnan(got[~rows])), what
+            assert_close(got[rows], want[rows], what)
+
+
 def test_attention_rejects_bad_args(gpu):
     rp, ci = random_csr(40, 3, 1)
     p = Problem(gpu, rp, ci)
