@@ -13,18 +13,22 @@
 //     (baselines/cpu_baseline.cpp:16-91).
 //
 // Work decomposition (one wave = one (item, head)):
-//   An item is a row window or, in a plan, a segment of a heavy window.
-//   MASKED: the wave expands its tiles into a list of attended columns
-//   ("slots"), each with the mask of the window rows that attend it, held in
-//   a per-wave LDS ring: 64 tiles per step, one tile per lane, positions from
-//   a DPP wave prefix sum.  Columns no row attends are never gathered (column
-//   compaction).  TILE_DENSE: a chunk is simply two whole tiles, i.e. 32
-//   columns in two runs of 16 contiguous K/V rows.  Slots are consumed 32 at
-//   a time (chunk_step):
-//     S^T[32 x 16] = K_slots[32 x 64] . Q_w^T    4 MFMA 16x16x32 (K gathered
-//                                                straight into A operands)
+//   An item is a row window or, in a plan, a segment of a heavy window; on
+//   small graphs a team of 4 or 16 waves of one workgroup shares a window
+//   (each wave a part of its tiles) and merges in LDS.
+//   MASKED, unplanned: the wave expands its tiles into a list of attended
+//   columns ("slots"), each with the mask of the window rows that attend it,
+//   held in a per-wave LDS ring: 64 tiles per step, one tile per lane,
+//   positions from a DPP wave prefix sum.  Columns no row attends are never
+//   gathered (column compaction).  MASKED with a compiled plan: the same
+//   lists, built once per graph, are read 32 columns per record.
+//   TILE_DENSE: a chunk is simply two whole tiles, i.e. 32 columns in two
+//   runs of 16 contiguous K/V rows.  Slots are consumed 32 at a time
+//   (chunk_step), their K and V rows gathered eight lanes per 128-byte row
+//   and handed to the matrix cores through a per-wave LDS stage:
+//     S^T[32 x 16] = K_slots[32 x 64] . Q_w^T    4 MFMA 16x16x32
 //     masked online softmax, row r in lanes r, r+16, r+32, r+48
-//     O^T[64 x 16] += V_slots^T . P^T            4 MFMA (V staged in LDS)
+//     O^T[64 x 16] += V_slots^T . P^T            4 MFMA
 //   Computing S^T instead of S puts each lane's logits for row r = lane%16
 //   exactly where the B operand of the P.V product needs them, and the O^T
 //   accumulator rows of a lane are also row r, so the per-row rescale
