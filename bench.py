@@ -225,7 +225,13 @@ def main() -> int:
 
     nbytes = alg_bytes(n, bsf.W, bsf.T, occ_sum, H, d, masked)
     achieved = nbytes / (kavg * 1e-3) / 1e9
+    # matrix-core work: the survey's tile model (4 products of 16x16x64 per
+    # active tile and head), and what the pass issues -- 8 MFMA 16x16x32 per
+    # chunk of 32 gathered columns (masked: the attended columns, at least
+    # occ_sum / 32 chunks; tile-dense: two tiles per chunk)
     flops_tile = bsf.T * 4 * 16 * 16 * d * H
+    chunks = (occ_sum + 31) // 32 if masked else (bsf.T + 1) // 2
+    flops_issued = chunks * H * 8 * (2 * 16 * 16 * 32)
     traffic = read_traffic(c.cfg, masked and not args.no_compile and args.order == "auto"
                            and args.seg == 0 and not args.heads)
     res = {
@@ -253,6 +259,7 @@ def main() -> int:
                       "median": float(np.median(kern_ms)) * 1e3, "cold_first_launch": cold_ms * 1e3},
         "alg_bytes_per_launch": nbytes,
         "mfma_frac_tile_model": flops_tile / (kavg * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
+        "mfma_frac_issued": flops_issued / (kavg * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
         "converter_us": conv_ms * 1e3,
         "converter_end_to_end_us": conv_e2e_ms * 1e3,
         "plan_us": plan_ms * 1e3,

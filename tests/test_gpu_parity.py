@@ -577,6 +577,7 @@ def test_config4_full_size(gpu):
         gpu.synchronize()
         got = dO.numpy()
         assert np.all(np.isfinite(got)), "unwritten or non-finite rows"
+        worst = (0.0, 0.0)
         for (a, b) in ranges:
             if masked:
                 want = orc.masked_attention(n, 64, 1, Qf, Kf, Vf, rp, ci, 1.0, a, b)[a:b]
@@ -585,7 +586,9 @@ def test_config4_full_size(gpu):
                                                 hb.block_col_indices, 1.0, a, b)[a:b]
             mabs, mrel = errors(got[a:b], want)
             assert mabs <= ABS_TOL and mrel <= REL_TOL, f"rows {a}:{b} masked={masked}: {mabs} {mrel}"
-        log(f"cfg4 masked={masked}: {len(ranges)} row ranges within tolerance")
+            worst = (max(worst[0], mabs), max(worst[1], mrel))
+        log(f"cfg4 masked={masked}: {len(ranges)} row ranges within tolerance, "
+            f"worst max_abs={worst[0]:.3e} max_rel={worst[1]:.3e}")
 
 
 @pytest.mark.slow
@@ -608,13 +611,21 @@ def test_config5_full_size(gpu):
     Qf, Kf, Vf = (x.astype(np.float32) for x in (Q, K, V))
     plan = gpu.Plan(bsf, None, H=H)
     plan.compile()
-    dO.fill_bytes(0xFF)
-    plan.forward(dQ, dK, dV, dO, masked=True)
-    gpu.synchronize()
-    got = dO.numpy()
-    assert np.all(np.isfinite(got))
-    for (a, b) in ranges:
-        want = orc.masked_attention(n, 64, H, Qf, Kf, Vf, rp, ci, 1.0, a, b)[a:b]
-        mabs, mrel = errors(got[a:b], want)
-        assert mabs <= ABS_TOL and mrel <= REL_TOL, f"rows {a}:{b}: {mabs} {mrel}"
-    log(f"cfg5 masked: {len(ranges)} row ranges ({len(rows)} rows) within tolerance")
+    for masked in (True, False):
+        dO.fill_bytes(0xFF)
+        plan.forward(dQ, dK, dV, dO, masked=masked)
+        gpu.synchronize()
+        got = dO.numpy()
+        assert np.all(np.isfinite(got))
+        worst = (0.0, 0.0)
+        for (a, b) in ranges:
+            if masked:
+                want = orc.masked_attention(n, 64, H, Qf, Kf, Vf, rp, ci, 1.0, a, b)[a:b]
+            else:
+                want = orc.tile_dense_attention(n, 64, H, Qf, Kf, Vf, hb.window_offsets,
+                                                hb.block_col_indices, 1.0, a, b)[a:b]
+            mabs, mrel = errors(got[a:b], want)
+            assert mabs <= ABS_TOL and mrel <= REL_TOL, f"rows {a}:{b} masked={masked}: {mabs} {mrel}"
+            worst = (max(worst[0], mabs), max(worst[1], mrel))
+        log(f"cfg5 masked={masked}: {len(ranges)} row ranges ({len(rows)} rows) within tolerance, "
+            f"worst max_abs={worst[0]:.3e} max_rel={worst[1]:.3e}")
