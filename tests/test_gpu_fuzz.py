@@ -1,6 +1,6 @@
 """Randomised parity sweep (deterministic seeds): graphs of random size and
-density with optional hub rows and isolated nodes, random head counts and
-scales, every launch shape -- unplanned in natural, sorted and random window
+density with optional hub rows and isolated nodes, converted bit-exactly,
+then random head counts and scales through every launch shape -- unplanned in natural, sorted and random window
 order, automatic plans (teams on small graphs), plans with small forced
 segments, compiled lists -- in both semantics, against the CPU oracle at the
 north-star bar (max abs 2e-3, normwise max rel 1e-2).
@@ -56,6 +56,10 @@ def test_random_parity(gpu, seed):
               "random": gpu.DeviceArray.from_numpy(r.permutation(W).astype(np.int32))}
     seg = int(r.integers(2, 64))
     hb = bsf.to_host()
+    offs, bcol, mask = orc.convert(n, rp, ci)   # the converter, bit-exact
+    assert np.array_equal(hb.window_offsets, offs)
+    assert np.array_equal(hb.block_col_indices, bcol)
+    assert np.array_equal(hb.tile_masks, mask)
     f = lambda x: x.astype(np.float32)
     print(f"seed {seed}: n={n} nnz={len(ci)} W={W} T={bsf.T} H={H} scale={scale} seg={seg}",
           flush=True)
