@@ -116,6 +116,13 @@ fused_attention_kernel(const AttnParams p)
         const int32_t T = p.window_offsets[p.W];
         tb = max(0, min(p.window_offsets[w], T));
         te = max(tb, min(p.window_offsets[w + 1], T));
+        if (p.heavy_mode) {
+            // the heavy windows among the first heavy_max order positions
+            // belong to the team launch (mode 2), all others to the one-wave
+            // launch (mode 1); uniform over a team's workgroup
+            const bool heavy = wi < p.heavy_max && te - tb > heavy_tiles(T, p.W);
+            if (heavy != (p.heavy_mode == 2)) return;
+        }
         if constexpr (TEAM > 1) {
             const int32_t a = team_part(tb, te, wave, TEAM), b = team_part(tb, te, wave + 1, TEAM);
             tb = a;
@@ -757,7 +764,26 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
     p.W = W;
     p.n = n;
     p.xcd_contiguous = d_window_order == nullptr;
-    return launch(p, H, scale, as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    if (p.team == 1 && d_window_order && !wide_features(n, H)) {
+        // Without a plan a hub window would run on one wave.  Given a window
+        // order, two launches instead: teams of 16 waves for the heavy
+        // windows among the first kHeavyMaxWindows order positions (the
+        // reference's descending order puts the hubs there), then one wave
+        // per window for all others.  Each window belongs to exactly one
+        // launch whatever the order.  (In natural order the hubs are
+        // anywhere, and the extra launch measured a little slower.)
+        const int32_t K = W < kHeavyMaxWindows ? W : kHeavyMaxWindows;
+        AttnParams ph = p;
+        ph.team = kTeamLarge;
+        ph.num_items = (int64_t)K * kTeamLarge;
+        ph.heavy_mode = 2;
+        ph.heavy_max = K;
+        F3S_TRY(launch(ph, H, scale, st));
+        p.heavy_mode = 1;
+        p.heavy_max = K;
+    }
+    return launch(p, H, scale, st);
 }
 
 f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_window_order,

@@ -68,7 +68,23 @@ struct AttnParams {
     const int32_t* chunk_base;       // compiled plan: item i owns chunks [cb[i], cb[i+1])
     const uint32_t* columns;         // compiled plan: per chunk 32 row offsets, 32 row masks
     int32_t team;                    // waves per window (1, or kTeamSmall / kTeamLarge)
+    int32_t heavy_mode;              // unplanned launches: 0 all windows; 1 all but the heavy
+                                     // windows among the first heavy_max order positions;
+                                     // 2 only those (teams)
+    int32_t heavy_max;
 };
+
+// A window is heavy for the unplanned two-launch schedule when its tiles
+// exceed both kHeavyMinTiles and kHeavyMeanFactor times the mean window.
+constexpr int32_t kHeavyMinTiles = 1024;
+constexpr int32_t kHeavyMeanFactor = 8;
+constexpr int32_t kHeavyMaxWindows = 512;   // order positions the team launch covers
+__host__ __device__ __forceinline__ int32_t heavy_tiles(int32_t T, int32_t W)
+{
+    const int64_t mean = W > 0 ? ((int64_t)T + W - 1) / W : 0;
+    const int64_t thr = mean * kHeavyMeanFactor;
+    return (int32_t)(thr > kHeavyMinTiles ? thr : kHeavyMinTiles);
+}
 
 // Small graphs: a team of waves in one workgroup shares each row window, each
 // wave taking an even share of the window's tiles (cut at tile pairs, the

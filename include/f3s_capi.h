@@ -116,9 +116,13 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * attended column get 0.  Requires d == 64 and 1 <= H <= 64 heads in
  * node-major [n][H][64] layout, of any size (tensors past ~4 GiB are read
  * with 64-bit addresses); scale = 1 reproduces the reference (which has no
- * scaling, and one head).  Small graphs (W*H <= 2048) run each window on a
- * team of 16 (W*H <= 512) or 4 waves of one workgroup, each wave taking an
- * even share of the window's tiles, merged in LDS in a fixed order. */
+ * scaling, and one head).  Small graphs run each window on a team of 4 or
+ * 16 waves of one workgroup (masked: W*H <= 1024, teams of 4; tile-dense:
+ * W*H <= 512, teams of 16, up to 2048, teams of 4), each wave taking an even
+ * share of the window's tiles, merged in LDS in a fixed order.  On larger
+ * graphs, given d_window_order, the heavy windows among its first 512
+ * entries (more than max(1024, 8 x mean) tiles) run as teams of 16 in a
+ * launch of their own before the others. */
 f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                              float* O, const int32_t* d_window_offsets,
                              const int32_t* d_block_col, const uint16_t* d_tile_mask,

@@ -472,6 +472,34 @@ def test_concurrent_streams_and_threads(gpu):
         assert np.array_equal(outs[k].view(np.uint32), want.view(np.uint32))
 
 
+def test_unplanned_heavy_windows(gpu):
+    # Without a plan but with a window order, windows of more than
+    # max(1024, 8 x mean) tiles among the first 512 order positions run as
+    # 16-wave teams in a launch of their own; every other window runs on one
+    # wave in the second launch (and all do in natural order).  Hubs sit in
+    # windows 0, 1 and 562 (1,250 tiles each); the orders put them first
+    # (sorted) or at positions 700, 5 and 100 (one of them past 512).
+    rp, ci = star_graph(20000, hubs=(0, 3, 17, 9000))
+    p = Problem(gpu, rp, ci, H=2, normal=True, seed=61)
+    W = p.bsf.W
+    offs = p.bsf.window_offsets.numpy()
+    tiles = np.diff(offs)
+    thr = max(1024, 8 * ((int(offs[-1]) + W - 1) // W))
+    heavy = np.nonzero(tiles > thr)[0]
+    assert list(heavy) == [0, 1, 562]
+    perm = rng(62).permutation(W).astype(np.int32)
+    for w, pos in ((0, 700), (1, 5), (562, 100)):      # move the hubs to chosen positions
+        j = int(np.nonzero(perm == w)[0][0])
+        perm[j], perm[pos] = perm[pos], perm[j]
+    orders = {"natural": None, "sorted": gpu.window_order_device(p.bsf),
+              "moved": gpu.DeviceArray.from_numpy(perm)}
+    for masked in (True, False):
+        want = p.oracle(masked, scale=0.125)
+        for name, order in orders.items():
+            got = p.run(masked, order=order, scale=0.125)
+            assert_close(got, want, f"unplanned heavy windows masked={masked} order={name}")
+
+
 @pytest.mark.parametrize("H", [1, 16])
 def test_window_order_with_invalid_entries(gpu, H):
     # A caller's window order may name invalid windows (< 0 or >= W): they
