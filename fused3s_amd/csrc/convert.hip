@@ -6,24 +6,29 @@
 // window_offsets = exclusive prefix of the set sizes (:39).  New output: the
 // 16 row masks of each tile (bit c of row r <=> edge (16w+r, 16b+c)).
 //
-// Design (one workgroup of 256 threads per window, no sort):
-//   * the window's block columns are marked in an LDS bitmap (one bit per
-//     block column, LDS atomic OR).  An edge that sets a new bit is a new
-//     tile, so the count pass needs no scan at all;
-//   * the fill pass also marks, in a 64-word summary, which bitmap words are
-//     non-empty, lists those words in ascending order, and scans their
-//     popcounts: a tile's rank (its output position) is the base of its word
-//     plus the set bits below it.  Block columns are written while walking
-//     the set bits; each edge then ORs its bit into the LDS mask of its tile
-//     and the masks are streamed out, kMaskTiles tiles at a time;
-//   * each thread owns a contiguous run of the window's edges and merges
-//     consecutive edges that hit the same LDS word before its atomic, so rows
-//     with sorted columns issue few atomics;
-//   * graphs wider than one bitmap (kSliceCols block columns) are swept in
-//     slices, and only slices that hold one of the window's edges are
-//     visited; bitmap words are cleared edge by edge after use;
-//   * edges stay in registers between phases when the window has at most
-//     kRegEdges of them; heavier (hub) windows re-read them from memory.
+// Design (no sort; an LDS bitmap with one bit per block column):
+//   * convert_light, the main pass: a persistent kernel (as many 256-thread
+//     workgroups as are resident at once) walks the windows of up to
+//     kLightEdges edges on graphs whose block columns fit one bitmap sized
+//     to the graph (up to 4.2 M nodes).  Every edge ORs its block column's
+//     bit into the bitmap; a bit set for the first time is a new tile, so
+//     the count pass needs no scan.  The fill pass marks non-empty bitmap
+//     words in a summary, turns it into word bases (a tile's output rank is
+//     the base of its word plus the set bits below it), stages the row masks
+//     and block columns of up to kMaskTiles tiles in LDS and streams them
+//     out in coalesced stores.  Each workgroup keeps the loads of its next
+//     window in flight while it works on the current one, and its barriers
+//     order LDS only, so they do not wait for those loads;
+//   * convert_hubs: the windows with more edges (listed by convert_light),
+//     one 1024-thread workgroup each -- or, on graphs too wide for one
+//     bitmap, every window with 256 threads, the bitmap swept in column
+//     slices of kSliceCols block columns (only slices holding an edge of the
+//     window are visited).  Each thread owns a contiguous run of the
+//     window's edges and merges consecutive edges that hit the same LDS word
+//     before its atomic; windows with more than NT * kEPT edges re-read them
+//     from memory and OR their masks straight into the zeroed output;
+//   * bitmap words are cleared edge by edge after use, so no pass touches
+//     all W / 32 words per window.
 // The per-window work is O(E) plus a few barriers; the output is
 // deterministic and does not depend on the order of columns in a row.
 // Counts are scanned into window_offsets with the device scan of runtime.hip.
@@ -34,14 +39,15 @@
 
 namespace f3s {
 
-constexpr int kConvThreads = 256;
+constexpr int kConvThreads = 256;                 // persistent kernel; per-window fallback
+constexpr int kHubThreads = 1024;                 // hub windows
 constexpr int kBitWords = 2048;                   // bitmap words per column slice
 constexpr int kSumWords = kBitWords / 32;         // summary: one bit per bitmap word
 constexpr int kSliceCols = kBitWords * 32;        // block columns per slice
 constexpr int kMaxSlices = 2048;                  // >= ceil(2^27 / kSliceCols)
 constexpr int kMaskTiles = 256;                   // tile masks staged in LDS at once
 constexpr int kEPT = 8;                           // edges per thread kept in registers
-constexpr int kRegEdges = kConvThreads * kEPT;
+constexpr int kHubBatch = 4;                      // edge loads in flight per thread, hub windows
 static_assert(kSumWords == kWave, "the summary is scanned by one wave");
 
 enum ConvErr : int32_t { kErrNone = 0, kErrRowPtr = 1, kErrCol = 2, kErrCount = 4 };
@@ -56,7 +62,7 @@ struct ConvLds {
     uint32_t summary[FILL ? kSumWords : 1];    // non-empty bitmap words
     uint32_t slices[kMaxSlices / 32];          // slices holding at least one edge
     int32_t rp[17];
-    int32_t scan[kConvThreads / kWave];
+    int32_t scan[kHubThreads / kWave];
     int32_t nlist;
     int32_t bad;
 };
@@ -66,7 +72,7 @@ struct WindowRows {
     int64_t e0, E;
 };
 
-// Loads the window's row pointers into LDS and validates them.
+// Loads the window's row pointers into LDS and validates them (threads 0-16).
 __device__ __forceinline__ WindowRows load_window_rows(const int32_t* __restrict__ row_ptr,
                                                        int32_t n, int64_t nnz, int32_t w,
                                                        int32_t* rp, int32_t* err)
@@ -78,7 +84,7 @@ __device__ __forceinline__ WindowRows load_window_rows(const int32_t* __restrict
     __syncthreads();
     if ((int)threadIdx.x < wr.nrows) {
         int32_t a = rp[threadIdx.x], b = rp[threadIdx.x + 1];
-        if (a < 0 || b < a || b > nnz) *err = kErrRowPtr;
+        if (a < 0 || b < a || b > nnz) atomicOr(err, kErrRowPtr);
     }
     wr.e0 = rp[0];
     wr.E = (int64_t)rp[wr.nrows] - wr.e0;
@@ -96,21 +102,24 @@ __device__ __forceinline__ int row_of_edge(const int32_t* rp, int nrows, int32_t
     return r;
 }
 
-// Pass kind: COUNT writes counts[w]; FILL writes block_col / tile_mask at
-// window_offsets[w] and checks the count against the offsets.
-template <bool FILL>
-__global__ void __launch_bounds__(kConvThreads)
-convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_idx,
-                int32_t n, int64_t nnz, int32_t W, int32_t* __restrict__ counts,
-                const int32_t* __restrict__ window_offsets, int32_t* __restrict__ block_col,
-                uint16_t* __restrict__ tile_mask, int32_t* __restrict__ err)
+// One window by one workgroup of NT threads, any edge count (the hub windows
+// the persistent kernel hands over, or every window of a graph too wide for
+// its bitmap).  Pass kind: COUNT writes counts[w]; FILL
+// writes block_col / tile_mask at window_offsets[w] and checks the count
+// against the offsets.
+template <bool FILL, int NT>
+__device__ __forceinline__ void
+convert_one_window(ConvLds<FILL>& L, int32_t w, const int32_t* __restrict__ row_ptr,
+                   const int32_t* __restrict__ col_idx, int32_t n, int64_t nnz, int32_t W,
+                   int32_t* __restrict__ counts, const int32_t* __restrict__ window_offsets,
+                   int32_t* __restrict__ block_col, uint16_t* __restrict__ tile_mask,
+                   int32_t* __restrict__ err)
 {
-    __shared__ ConvLds<FILL> L;
-    const int32_t w = blockIdx.x;
     const int tid = threadIdx.x;
+    __syncthreads();   // the previous window of this workgroup is done with L
     if (tid == 0) L.bad = 0;
     if (tid < kMaxSlices / 32) L.slices[tid] = 0u;
-    for (int g = tid; g < kBitWords / 4; g += kConvThreads)
+    for (int g = tid; g < kBitWords / 4; g += NT)
         *reinterpret_cast<uint4*>(&L.bits[4 * g]) = make_uint4(0u, 0u, 0u, 0u);
     if constexpr (FILL) {
         if (tid < kSumWords) L.summary[tid] = 0u;
@@ -118,7 +127,7 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
     WindowRows wr = load_window_rows(row_ptr, n, nnz, w, L.rp, err);
     __syncthreads();
     if (wr.E < 0 || wr.e0 < 0 || wr.e0 + wr.E > nnz) {
-        if (tid == 0) *err = kErrRowPtr;
+        if (tid == 0) atomicOr(err, kErrRowPtr);
         return;
     }
     int32_t out_base = 0, expect = 0;
@@ -130,17 +139,18 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
         out_base = window_offsets[w];
         expect = window_offsets[w + 1] - out_base;
         if (out_base < 0 || expect < 0 || out_base > total - expect) {
-            if (tid == 0) *err = kErrCount;
+            if (tid == 0) atomicOr(err, kErrCount);
             return;
         }
     }
+    constexpr int kRegEdgesNT = NT * kEPT;
     const int E = (int)wr.E;
     const int32_t e0 = (int32_t)wr.e0;
     const int nrows = wr.nrows;
     // This thread's run of edges: e0 + [i0, i1).
-    const int per = (E + kConvThreads - 1) / kConvThreads;
+    const int per = (E + NT - 1) / NT;
     const int i0 = min(E, tid * per), i1 = min(E, i0 + per);
-    const bool in_regs = E <= kRegEdges;   // i.e. per <= kEPT
+    const bool in_regs = E <= kRegEdgesNT;   // i.e. per <= kEPT
 
     // Visits the run's valid edges (column c, row r) in order.
     int32_t col[kEPT];
@@ -151,11 +161,20 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
             for (int j = 0; j < kEPT; ++j)
                 if (col[j] >= 0) fn(col[j], (int)((rows >> (4 * j)) & 15u));
         } else {
+            // kHubBatch loads in flight per thread, then their edges in order
             int r = i0 < i1 ? row_of_edge(L.rp, nrows, e0 + i0) : 0;
-            for (int i = i0; i < i1; ++i) {
-                while (r + 1 < nrows && e0 + i >= L.rp[r + 1]) ++r;
-                const int32_t c = col_idx[e0 + i];
-                if (c >= 0 && c < n) fn(c, r);
+            for (int i = i0; i < i1; i += kHubBatch) {
+                int32_t cb[kHubBatch];
+#pragma unroll
+                for (int j = 0; j < kHubBatch; ++j)
+                    cb[j] = i + j < i1 ? col_idx[e0 + i + j] : -1;
+#pragma unroll
+                for (int j = 0; j < kHubBatch; ++j) {
+                    if (i + j < i1) {
+                        while (r + 1 < nrows && e0 + i + j >= L.rp[r + 1]) ++r;
+                        if (cb[j] >= 0 && cb[j] < n) fn(cb[j], r);
+                    }
+                }
             }
         }
     };
@@ -190,12 +209,18 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
                 rows |= (uint32_t)r << (4 * j);
             }
         } else {
-            for (int i = i0; i < i1; ++i) {
-                const int32_t c = col_idx[e0 + i];
-                if (c < 0 || c >= n)
-                    L.bad = 1;
-                else
-                    mark(c);
+            for (int i = i0; i < i1; i += kHubBatch) {
+                int32_t cb[kHubBatch];
+#pragma unroll
+                for (int j = 0; j < kHubBatch; ++j)
+                    cb[j] = i + j < i1 ? col_idx[e0 + i + j] : 0;
+#pragma unroll
+                for (int j = 0; j < kHubBatch; ++j) {
+                    if (cb[j] < 0 || cb[j] >= n)
+                        L.bad = 1;
+                    else
+                        mark(cb[j]);
+                }
             }
         }
     }
@@ -234,7 +259,7 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
             flush();
         }
         int32_t total;
-        (void)block_exclusive_scan<kConvThreads>(fresh, L.scan, total);   // barriers inside
+        (void)block_exclusive_scan<NT>(fresh, L.scan, total);   // barriers inside
 
         if constexpr (FILL) {
             if (running + total <= expect) {
@@ -254,12 +279,12 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
                 __syncthreads();
                 // ---- word bases and block columns, contiguous list entries ----
                 const int nl = L.nlist;
-                const int lper = (nl + kConvThreads - 1) / kConvThreads;
+                const int lper = (nl + NT - 1) / NT;
                 const int a0 = min(nl, tid * lper), a1 = min(nl, a0 + lper);
                 int32_t loc = 0;
                 for (int a = a0; a < a1; ++a) loc += __popc(L.bits[L.list[a]]);
                 int32_t tot2;
-                int32_t t = block_exclusive_scan<kConvThreads>(loc, L.scan, tot2);
+                int32_t t = block_exclusive_scan<NT>(loc, L.scan, tot2);
                 for (int a = a0; a < a1; ++a) {
                     const int wi = L.list[a];
                     L.base[wi] = (uint32_t)t;
@@ -278,7 +303,7 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
                     if (tile_mask) {
                         uint4* dst = reinterpret_cast<uint4*>(
                             tile_mask + ((int64_t)out_base + running) * 16);
-                        for (int i = tid; i < 2 * total; i += kConvThreads)
+                        for (int i = tid; i < 2 * total; i += NT)
                             dst[i] = make_uint4(0u, 0u, 0u, 0u);
                         // the zeros reach L2, where the atomics act, before any OR
                         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -307,7 +332,7 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
                 }
                 // ---- tile masks, kMaskTiles at a time ----
                 for (int32_t ms = 0; in_regs && ms < total; ms += kMaskTiles) {
-                    for (int i = tid; i < kMaskTiles * 2; i += kConvThreads)
+                    for (int i = tid; i < kMaskTiles * 2; i += NT)
                         *reinterpret_cast<uint4*>(&L.masks[4 * i]) = make_uint4(0u, 0u, 0u, 0u);
                     __syncthreads();
                     int32_t cur = -1;
@@ -332,7 +357,7 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
                     __syncthreads();
                     if (tile_mask) {
                         const int32_t nt = min(kMaskTiles, total - ms);
-                        for (int t3 = tid; t3 < nt; t3 += kConvThreads) {
+                        for (int t3 = tid; t3 < nt; t3 += NT) {
                             const uint4* src = reinterpret_cast<const uint4*>(&L.masks[t3 * 8]);
                             uint4* dst = reinterpret_cast<uint4*>(
                                 tile_mask + ((int64_t)out_base + running + ms + t3) * 16);
@@ -354,13 +379,464 @@ convert_windows(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__
         __syncthreads();
     }
     if (tid == 0) {
-        if (L.bad) *err = kErrCol;
+        if (L.bad) atomicOr(err, kErrCol);
         if (FILL) {
-            if (running != expect) *err = kErrCount;
+            if (running != expect) atomicOr(err, kErrCount);
         } else {
             counts[w] = running;
         }
     }
+}
+
+// The hub windows listed by convert_light (hubs != NULL), or every window
+// (hubs == NULL: graphs too wide for convert_light's bitmap); a workgroup per
+// window.
+template <bool FILL, int NT>
+__global__ void __launch_bounds__(NT)
+convert_hubs(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_idx,
+             int32_t n, int64_t nnz, int32_t W, int32_t* __restrict__ counts,
+             const int32_t* __restrict__ window_offsets, int32_t* __restrict__ block_col,
+             uint16_t* __restrict__ tile_mask, const int32_t* __restrict__ hubs,
+             const int32_t* __restrict__ num_hubs, int32_t* __restrict__ err)
+{
+    __shared__ ConvLds<FILL> L;
+    const int32_t nh = hubs ? *num_hubs : W;
+    for (int32_t i = blockIdx.x; i < nh; i += gridDim.x) {
+        const int32_t w = hubs ? hubs[i] : i;
+        if (w < 0 || w >= W) continue;   // uniform
+        convert_one_window<FILL, NT>(L, w, row_ptr, col_idx, n, nnz, W, counts, window_offsets,
+                                 block_col, tile_mask, err);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent kernel for the windows with at most kLightEdges edges, on graphs
+// whose block columns fit one LDS bitmap (W <= 32 kLightMaxWords).
+//
+// Each workgroup walks windows w_i = blockIdx.x + i G (G = grid size) and
+// keeps its memory traffic one window ahead of its work: while it works on
+// w_i, the edges of w_{i+1} are in flight into a second register set, and
+// the row pointers (and, when filling, output offsets) of w_{i+3} into a
+// register; those of w_{i+2}, fetched one window earlier, go into a
+// three-slot LDS ring.  The bitmap (one bit per block column, sized to the
+// graph) stays clear between windows: each edge clears its own word after
+// use.  Per window:
+//   mark   every edge ORs its block column's bit into the bitmap; a bit set
+//          for the first time is a new tile (count); the first setter of a
+//          word also marks the word in the summary (fill);
+//   base   (fill) wave 0 turns the summary into word bases: a tile's output
+//          rank is the base of its word plus the set bits below it;
+//   stage  (fill) every edge ORs its bit into its tile's staged row masks and
+//          records the tile's block column, kMaskTiles tiles per round; each
+//          thread then streams out (and re-zeroes) the tiles it owns, so
+//          block columns and masks leave in coalesced stores;
+//   clear  every edge clears its bitmap word.
+// The per-edge work is a handful of VALU operations and one or two LDS
+// atomics: the pass is bound by instruction issue, so it keeps no per-edge
+// state beyond the column (and, filling, the row).  Windows with more edges
+// are listed for convert_hubs, so that one heavy window never holds up the
+// windows queued behind it in this workgroup.
+// ---------------------------------------------------------------------------
+constexpr int kLightEPT = 4;                      // edges per thread, light windows
+constexpr int kLightEdges = kConvThreads * kLightEPT;
+constexpr int kLightMaxWords = 8192;              // bitmap words: W <= 262,144 (n <= 4,194,304)
+constexpr int kMetaInts = 20;                     // rp[0..16], out_base, expect, flags
+constexpr int kMetaSlots = 3;                     // windows w_i, w_{i+1}, w_{i+2}
+constexpr int kMiscInts = 8;                      // cnt[2], total[2], bad
+constexpr int kFlagLive = 1, kFlagRowsOk = 2, kFlagOutOk = 4;
+
+// Dynamic LDS layout of convert_light (bytes; 16-byte aligned sections).
+struct LightLayout {
+    int32_t words;   // bitmap words, ceil(W / 32)
+    int32_t sums;    // summary words, ceil(words / 32) (fill)
+    uint32_t off_base, off_sum, off_masks, off_tcol, off_meta, bytes;
+};
+
+__host__ __device__ inline uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
+
+__host__ __device__ inline LightLayout light_layout(int32_t W, bool fill)
+{
+    LightLayout l;
+    l.words = (W + 31) / 32;
+    l.sums = (l.words + 31) / 32;
+    uint32_t o = align16(4u * (uint32_t)l.words);
+    l.off_base = o;
+    if (fill) o = align16(o + 2u * (uint32_t)l.words);
+    l.off_sum = o;
+    if (fill) o = align16(o + 4u * (uint32_t)l.sums);
+    l.off_masks = o;
+    if (fill) o = align16(o + 4u * kMaskTiles * 8);
+    l.off_tcol = o;
+    if (fill) o = align16(o + 4u * kMaskTiles);
+    l.off_meta = o;
+    o = align16(o + 4u * (kMetaSlots * kMetaInts + kMiscInts));
+    l.bytes = o;
+    return l;
+}
+
+extern __shared__ __align__(16) unsigned char conv_lds[];
+
+struct LightLds {
+    uint32_t* bits;     // [words] block columns of the window
+    uint16_t* base;     // [words] tiles before each word (fill)
+    uint32_t* summary;  // [sums] non-empty bitmap words (fill)
+    uint32_t* masks;    // [kMaskTiles * 8] staged row masks, two rows per word (fill)
+    int32_t* tcol;      // [kMaskTiles] staged block columns (fill)
+    int32_t* meta;      // [kMetaSlots][kMetaInts] window descriptions (ring)
+    int32_t* cnt;       // [2] count: tiles of a window, by parity
+    int32_t* total;     // [2] fill: tiles of a window, by parity
+    int32_t* bad;       // a column outside [0, n) was seen
+    int32_t words, sums;
+};
+
+__device__ __forceinline__ LightLds light_lds(const LightLayout& lay)
+{
+    LightLds L;
+    L.bits = reinterpret_cast<uint32_t*>(conv_lds);
+    L.base = reinterpret_cast<uint16_t*>(conv_lds + lay.off_base);
+    L.summary = reinterpret_cast<uint32_t*>(conv_lds + lay.off_sum);
+    L.masks = reinterpret_cast<uint32_t*>(conv_lds + lay.off_masks);
+    L.tcol = reinterpret_cast<int32_t*>(conv_lds + lay.off_tcol);
+    L.meta = reinterpret_cast<int32_t*>(conv_lds + lay.off_meta);
+    L.cnt = L.meta + kMetaSlots * kMetaInts;
+    L.total = L.cnt + 2;
+    L.bad = L.cnt + 4;
+    L.words = lay.words;
+    L.sums = lay.sums;
+    return L;
+}
+
+// What lane t (< 19) fetches for window wn: row_ptr[16 wn + t] for t <=
+// nrows, window_offsets[wn] (t = 17) and [wn + 1] (t = 18) when filling.
+// One vector load with a per-lane address (a uniform window_offsets load
+// would become a scalar load into the same register, and that register
+// write would have to wait for every load in flight).
+template <bool FILL>
+__device__ __forceinline__ int32_t fetch_meta(int32_t wn, int32_t W, int32_t n,
+                                              const int32_t* __restrict__ row_ptr,
+                                              const int32_t* __restrict__ window_offsets)
+{
+    const int t = threadIdx.x & (kWave - 1);
+    const int32_t* p = nullptr;
+    if (wn < W) {
+        const int nrows = min(16, n - wn * 16);
+        if (t <= nrows) p = row_ptr + (int64_t)wn * 16 + t;
+        if (FILL && (t == 17 || t == 18)) p = window_offsets + wn + (t - 17);
+    }
+    int32_t v = 0;
+    if (p) v = *p;
+    return v;
+}
+
+// Wave 0 stores a fetched window description into ring slot `slot`, with
+// flags: live (wn < W), row pointers usable (0 <= rp[0] <= ... <= rp[nrows]
+// <= nnz) and output range usable ([out_base, out_base + expect) inside
+// [0, total_tiles)).
+template <bool FILL>
+__device__ __forceinline__ void publish_meta(const LightLds& L, int slot, int32_t v, int32_t wn,
+                                             int32_t W, int32_t n, int64_t nnz,
+                                             int32_t total_tiles, int32_t* __restrict__ err)
+{
+    const int lane = threadIdx.x;   // wave 0 only
+    const bool live = wn < W;
+    const int nrows = live ? min(16, n - wn * 16) : 0;
+    const int32_t rp0 = __shfl(v, 0, kWave), rpn = __shfl(v, nrows, kWave);
+    const int32_t nxt = __shfl_down(v, 1, kWave);
+    const bool back = lane < nrows && nxt < v;
+    const bool rows_ok = live && !__any(back) && rp0 >= 0 && rpn >= rp0 && (int64_t)rpn <= nnz;
+    bool out_ok = true;
+    int32_t val = v;
+    if (FILL) {
+        // lanes 17 and 18 hold window_offsets[wn] and [wn + 1]
+        const int32_t ob = __shfl(v, 17, kWave), end = __shfl(v, 18, kWave);
+        out_ok = ob >= 0 && end >= ob && end <= total_tiles;
+        if (lane == 18) val = out_ok ? end - ob : 0;   // expect
+    }
+    int32_t* dst = L.meta + slot * kMetaInts;
+    if (lane < 19) dst[lane] = val;
+    if (lane == 19)
+        dst[19] = (live ? kFlagLive : 0) | (rows_ok ? kFlagRowsOk : 0) |
+                  (out_ok ? kFlagOutOk : 0) | (nrows << 8);
+    if (lane == 0 && live) {
+        if (!rows_ok) atomicOr(err, kErrRowPtr);
+        else if (!out_ok) atomicOr(err, kErrCount);
+    }
+}
+
+struct LightWin {
+    int32_t e0, E, nrows, out_base, expect, flags;
+};
+
+__device__ __forceinline__ LightWin read_meta(const LightLds& L, int slot)
+{
+    const int32_t* m0 = L.meta + slot * kMetaInts;
+    LightWin m;
+    m.flags = m0[19];
+    m.nrows = m.flags >> 8;
+    m.e0 = m0[0];
+    m.E = (m.flags & kFlagRowsOk) ? m0[m.nrows] - m.e0 : 0;
+    m.out_base = m0[17];
+    m.expect = m0[18];
+    return m;
+}
+
+// Issues the loads of this thread's run of edges of the window in ring slot
+// `slot` (nothing for hub windows): col[j] for j < cnt, and (filling) the
+// rows, packed 4 bits per edge.  The loaded values are not used here, so the
+// loads stay in flight.
+template <bool FILL>
+__device__ __forceinline__ void issue_edges(const LightLds& L, int slot,
+                                            const int32_t* __restrict__ col_idx,
+                                            int32_t (&col)[kLightEPT], uint32_t& rows, int& cnt)
+{
+    const LightWin m = read_meta(L, slot);
+    cnt = 0;
+    rows = 0;
+    if (m.E <= 0 || m.E > kLightEdges) return;
+    const int per = (m.E + kConvThreads - 1) / kConvThreads;
+    const int i0 = min(m.E, (int)threadIdx.x * per), i1 = min(m.E, i0 + per);
+    cnt = i1 - i0;
+#pragma unroll
+    for (int j = 0; j < kLightEPT; ++j)
+        if (j < cnt) col[j] = col_idx[m.e0 + i0 + j];
+    if (FILL && cnt > 0) {
+        const int32_t* rp = L.meta + slot * kMetaInts;
+        int r = row_of_edge(rp, m.nrows, m.e0 + i0);
+#pragma unroll
+        for (int j = 0; j < kLightEPT; ++j) {
+            const int32_t e = m.e0 + i0 + j;
+            while (r + 1 < m.nrows && e >= rp[r + 1]) ++r;
+            rows |= (uint32_t)r << (4 * j);
+        }
+    }
+}
+
+// One window (at most kLightEdges edges, in col / rows) described by ring
+// slot `slot`.  Every thread runs the same sequence of barriers.  Nothing
+// here waits for a load: the only loads in flight are the next window's.
+template <bool FILL>
+__device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_t w,
+                                             int32_t (&col)[kLightEPT], uint32_t rows, int cnt,
+                                             int& round, int32_t n,
+                                             int32_t* __restrict__ counts,
+                                             int32_t* __restrict__ block_col,
+                                             uint16_t* __restrict__ tile_mask,
+                                             int32_t* __restrict__ hubs,
+                                             int32_t* __restrict__ num_hubs,
+                                             int32_t* __restrict__ err)
+{
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wid = tid / kWave;
+    const LightWin m = read_meta(L, slot);
+    const bool usable = (m.flags & kFlagLive) && (m.flags & kFlagRowsOk) &&
+                        (!FILL || (m.flags & kFlagOutOk));
+
+    if (!usable || m.E > kLightEdges || m.E == 0) {
+        // hub (listed for convert_hubs), empty or rejected window: no tiles here
+        if (tid == 0) {
+            if (usable && m.E > 0) {
+                const int32_t i = atomicAdd(num_hubs, 1);
+                hubs[i] = w;
+            } else if (FILL) {
+                if (usable && m.expect != 0) atomicOr(err, kErrCount);
+            } else {
+                counts[w] = 0;
+            }
+        }
+        lds_barrier();   // the description published for window w + 2G is visible
+        return;
+    }
+
+    // absent (j >= cnt) and invalid columns become -1; an invalid column
+    // (outside [0, n)) is reported and left out
+#pragma unroll
+    for (int j = 0; j < kLightEPT; ++j) {
+        const int32_t c = col[j];
+        const bool present = j < cnt;
+        const bool ok = present && c >= 0 && c < n;
+        if (present && !ok) *L.bad = 1;
+        col[j] = ok ? c : -1;
+    }
+    const int k = round & 1;
+    ++round;
+
+    // ---- mark ----
+    int32_t fresh = 0;
+#pragma unroll
+    for (int j = 0; j < kLightEPT; ++j) {
+        const int32_t c = col[j];
+        if (c < 0) continue;
+        const int32_t wi = c >> 9;
+        const uint32_t bit = 1u << ((c >> 4) & 31);
+        const uint32_t old = atomicOr(&L.bits[wi], bit);
+        if (FILL) {
+            if (old == 0u) atomicOr(&L.summary[wi >> 5], 1u << (wi & 31));
+        } else {
+            fresh += (old & bit) == 0u;
+        }
+    }
+    if (!FILL) {
+        fresh = wave_sum(fresh);
+        if (lane == 0 && fresh) atomicAdd(&L.cnt[k], fresh);
+    }
+    lds_barrier();   // B1: bitmap (+ summary) complete
+    if (tid == 0) L.cnt[k ^ 1] = 0;   // read before B1 by the previous window
+
+    int32_t total;
+    if constexpr (!FILL) {
+        total = L.cnt[k];
+    } else {
+        // ---- base (wave 0): lane l owns summary words [l spl, (l + 1) spl) ----
+        if (wid == 0) {
+            const int spl = (L.sums + kWave - 1) / kWave;
+            const int s0 = min(L.sums, lane * spl), s1 = min(L.sums, s0 + spl);
+            int32_t own = 0;
+            for (int sw = s0; sw < s1; ++sw)
+                for (uint32_t t = L.summary[sw]; t; t &= t - 1u)
+                    own += __popc(L.bits[sw * 32 + __builtin_ctz(t)]);
+            const int32_t incl = wave_inclusive_scan(own);
+            int32_t t0 = incl - own;
+            for (int sw = s0; sw < s1; ++sw) {
+                uint32_t t = L.summary[sw];
+                if (!t) continue;
+                L.summary[sw] = 0u;
+                for (; t; t &= t - 1u) {
+                    const int wi = sw * 32 + __builtin_ctz(t);
+                    L.base[wi] = (uint16_t)t0;
+                    t0 += __popc(L.bits[wi]);
+                }
+            }
+            if (lane == kWave - 1) L.total[k] = incl;
+        }
+        lds_barrier();   // B2: bases and the window's tile count
+        total = L.total[k];
+        if (total <= m.expect) {
+            // ---- stage, kMaskTiles tiles per round ----
+            for (int32_t ms = 0; ms < total; ms += kMaskTiles) {
+                if (ms > 0) lds_barrier();   // the previous round's tiles are re-zeroed
+#pragma unroll
+                for (int j = 0; j < kLightEPT; ++j) {
+                    const int32_t c = col[j];
+                    if (c < 0) continue;
+                    const int32_t wi = c >> 9;
+                    const uint32_t below = (1u << ((c >> 4) & 31)) - 1u;
+                    const int32_t t2 = (int32_t)L.base[wi] + __popc(L.bits[wi] & below) - ms;
+                    if (t2 < 0 || t2 >= kMaskTiles) continue;
+                    const int r = (int)((rows >> (4 * j)) & 15u);
+                    atomicOr(&L.masks[t2 * 8 + (r >> 1)], (1u << (c & 15)) << (16 * (r & 1)));
+                    L.tcol[t2] = c >> 4;   // every edge of the tile writes the same value
+                }
+                lds_barrier();   // B3: the round's staged tiles are complete
+                const int32_t nt = min(kMaskTiles, total - ms);
+                for (int t3 = tid; t3 < nt; t3 += kConvThreads) {
+                    const int64_t o = (int64_t)m.out_base + ms + t3;
+                    block_col[o] = L.tcol[t3];
+                    uint4* src = reinterpret_cast<uint4*>(&L.masks[t3 * 8]);
+                    if (tile_mask) {
+                        uint4* dst = reinterpret_cast<uint4*>(tile_mask + o * 16);
+                        dst[0] = src[0];
+                        dst[1] = src[1];
+                    }
+                    src[0] = make_uint4(0u, 0u, 0u, 0u);
+                    src[1] = make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
+        }
+    }
+    // ---- clear (every reader of the bitmap is past B1, B2 or B3) ----
+#pragma unroll
+    for (int j = 0; j < kLightEPT; ++j)
+        if (col[j] >= 0) L.bits[col[j] >> 9] = 0u;
+    lds_barrier();   // B4: bitmap and staged masks clear for the next window
+    if (tid == 0) {
+        if (FILL) {
+            if (total != m.expect) atomicOr(err, kErrCount);
+        } else {
+            counts[w] = total;
+        }
+    }
+}
+
+template <bool FILL>
+__global__ void __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_eu(4, 8)))
+convert_light(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_idx,
+              int32_t n, int64_t nnz, int32_t W, int32_t* __restrict__ counts,
+              const int32_t* __restrict__ window_offsets, int32_t* __restrict__ block_col,
+              uint16_t* __restrict__ tile_mask, int32_t* __restrict__ hubs,
+              int32_t* __restrict__ num_hubs, int32_t* __restrict__ err)
+{
+    const LightLayout lay = light_layout(W, FILL);
+    const LightLds L = light_lds(lay);
+    const int tid = threadIdx.x;
+    const int wid = tid / kWave;
+    const int32_t G = gridDim.x;
+    int32_t w = blockIdx.x;
+    if (w >= W) return;   // uniform
+    for (int g = tid; g < (L.words + 3) / 4; g += kConvThreads)
+        *reinterpret_cast<uint4*>(&L.bits[4 * g]) = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (FILL) {
+        for (int g = tid; g < kMaskTiles * 2; g += kConvThreads)
+            *reinterpret_cast<uint4*>(&L.masks[4 * g]) = make_uint4(0u, 0u, 0u, 0u);
+        for (int g = tid; g < L.sums; g += kConvThreads) L.summary[g] = 0u;
+    }
+    if (tid < kMiscInts) L.cnt[tid] = 0;
+    const int32_t total_tiles = FILL ? window_offsets[W] : 0;
+    // descriptions in flight (every wave fetches them; wave 0 publishes)
+    int32_t aheadX = 0, aheadY = 0;
+    {
+        const int32_t v0 = fetch_meta<FILL>(w, W, n, row_ptr, window_offsets);
+        const int32_t v1 = fetch_meta<FILL>(w + G, W, n, row_ptr, window_offsets);
+        aheadX = fetch_meta<FILL>(w + 2 * G, W, n, row_ptr, window_offsets);
+        if (wid == 0) {
+            publish_meta<FILL>(L, 0, v0, w, W, n, nnz, total_tiles, err);
+            publish_meta<FILL>(L, 1, v1, w + G, W, n, nnz, total_tiles, err);
+        }
+    }
+    lds_barrier();
+
+    static_assert(kLightEPT == 4, "the register uses in the loop name every edge register");
+    int32_t colA[kLightEPT], colB[kLightEPT];
+    uint32_t rowsA = 0, rowsB = 0;
+    int cntA = 0, cntB = 0;
+    int round = 0;
+    int slot = 0;   // ring slot of the current window
+    issue_edges<FILL>(L, 0, col_idx, colA, rowsA, cntA);
+    // Two windows per trip so that the register sets alternate without copies
+    // (a copy would wait for the loads in flight).  Each half first uses the
+    // registers loaded one window ago -- gfx950 counts loads and stores with
+    // one counter, so once a store is pending any wait is a wait for
+    // everything, and it must come before the next window's loads issue --
+    // then publishes the description of w + 2G into the ring slot whose last
+    // readers (window w - G) are past a barrier, issues the loads of w + G
+    // and w + 3G, and works on w.
+    while (true) {
+        {
+            const int s1 = slot == 2 ? 0 : slot + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+            asm volatile("" ::"v"(colA[0]), "v"(colA[1]), "v"(colA[2]), "v"(colA[3]), "v"(aheadX));
+            if (wid == 0) publish_meta<FILL>(L, s2, aheadX, w + 2 * G, W, n, nnz, total_tiles, err);
+            aheadY = fetch_meta<FILL>(w + 3 * G, W, n, row_ptr, window_offsets);
+            issue_edges<FILL>(L, s1, col_idx, colB, rowsB, cntB);
+            light_window<FILL>(L, slot, w, colA, rowsA, cntA, round, n, counts, block_col,
+                               tile_mask, hubs, num_hubs, err);
+            w += G;
+            slot = s1;
+            if (w >= W) break;
+        }
+        {
+            const int s1 = slot == 2 ? 0 : slot + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+            asm volatile("" ::"v"(colB[0]), "v"(colB[1]), "v"(colB[2]), "v"(colB[3]), "v"(aheadY));
+            if (wid == 0) publish_meta<FILL>(L, s2, aheadY, w + 2 * G, W, n, nnz, total_tiles, err);
+            aheadX = fetch_meta<FILL>(w + 3 * G, W, n, row_ptr, window_offsets);
+            issue_edges<FILL>(L, s1, col_idx, colA, rowsA, cntA);
+            light_window<FILL>(L, slot, w, colB, rowsB, cntB, round, n, counts, block_col,
+                               tile_mask, hubs, num_hubs, err);
+            w += G;
+            slot = s1;
+            if (w >= W) break;
+        }
+    }
+    if (tid == 0 && *L.bad) atomicOr(err, kErrCol);
 }
 
 __global__ void offsets_to_i32(const int64_t* __restrict__ in, int32_t* __restrict__ out,
@@ -370,10 +846,51 @@ __global__ void offsets_to_i32(const int64_t* __restrict__ in, int32_t* __restri
     if (i < count) out[i] = (int32_t)in[i];
 }
 
-// Per-call workspace of the converter (counts, scan temporaries, flags).
+// Per-call workspace of the converter (counts, scan temporaries, the hub
+// window list, flags: error bits and the hub count).
 struct ConvertScratch {
-    DeviceBuffer counts, offs64, tmp, flags;
+    DeviceBuffer counts, offs64, tmp, hubs, flags;
 };
+
+// One pass (count or fill) over all windows: the persistent kernel with as
+// many workgroups as fit on the device at once, then the hub windows it
+// listed (the hub launch cannot know the hub count, so it loops over the
+// list with a fixed grid).  Graphs too wide for one LDS bitmap run every
+// window through the per-window kernel.
+template <bool FILL>
+static f3s_status launch_pass(const int32_t* row_ptr, const int32_t* col_idx, int32_t n,
+                              int64_t nnz, int32_t W, int32_t* counts,
+                              const int32_t* window_offsets, int32_t* block_col,
+                              uint16_t* tile_mask, int32_t* hubs, int32_t* num_hubs,
+                              int32_t* err, hipStream_t stream)
+{
+    if (W <= 0) return F3S_OK;
+    if ((int64_t)W > 32LL * kLightMaxWords) {
+        hipLaunchKernelGGL((convert_hubs<FILL, kConvThreads>), dim3((unsigned)W), dim3(kConvThreads), 0,
+                           stream, row_ptr, col_idx, n, nnz, W, counts, window_offsets,
+                           block_col, tile_mask, nullptr, nullptr, err);
+        F3S_HIP(hipGetLastError());
+        return F3S_OK;
+    }
+    const LightLayout lay = light_layout(W, FILL);
+    int dev = 0, cus = 0, per_cu = 0;
+    F3S_HIP(hipGetDevice(&dev));
+    F3S_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, convert_light<FILL>,
+                                                         kConvThreads, lay.bytes));
+    const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    const unsigned grid = (unsigned)(W < resident ? W : resident);
+    hipLaunchKernelGGL((convert_light<FILL>), dim3(grid), dim3(kConvThreads), lay.bytes, stream,
+                       row_ptr, col_idx, n, nnz, W, counts, window_offsets, block_col,
+                       tile_mask, hubs, num_hubs, err);
+    F3S_HIP(hipGetLastError());
+    const int64_t hub_grid = 2 * (int64_t)(cus > 0 ? cus : 1);
+    hipLaunchKernelGGL((convert_hubs<FILL, kHubThreads>), dim3((unsigned)(W < hub_grid ? W : hub_grid)),
+                       dim3(kHubThreads), 0, stream, row_ptr, col_idx, n, nnz, W, counts,
+                       window_offsets, block_col, tile_mask, hubs, num_hubs, err);
+    F3S_HIP(hipGetLastError());
+    return F3S_OK;
+}
 
 static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, int32_t n,
                                int64_t nnz, int32_t* window_offsets, int32_t* block_col,
@@ -382,20 +899,19 @@ static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, i
     const int32_t W = (int32_t)ceil_div(n, 16);
     ConvertScratch s;
     F3S_TRY(s.flags.reserve(sizeof(int32_t) * 2 + sizeof(int64_t)));
+    F3S_TRY(s.hubs.reserve(sizeof(int32_t) * ((size_t)W + 1)));
     int32_t* err = reinterpret_cast<int32_t*>(s.flags.ptr);
-    F3S_HIP(hipMemsetAsync(err, 0, sizeof(int32_t), stream));
+    int32_t* num_hubs = err + 1;
+    int32_t* hubs = reinterpret_cast<int32_t*>(s.hubs.ptr);
+    F3S_HIP(hipMemsetAsync(err, 0, 2 * sizeof(int32_t), stream));
 
     if (!block_col) {
         F3S_TRY(s.counts.reserve(sizeof(int32_t) * (size_t)W));
         F3S_TRY(s.offs64.reserve(sizeof(int64_t) * ((size_t)W + 1)));
         F3S_TRY(s.tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(W)));
         int32_t* counts = reinterpret_cast<int32_t*>(s.counts.ptr);
-        if (W > 0) {
-            hipLaunchKernelGGL((convert_windows<false>), dim3(W), dim3(kConvThreads), 0, stream,
-                               row_ptr, col_idx, n, nnz, W, counts, nullptr, nullptr, nullptr,
-                               err);
-            F3S_HIP(hipGetLastError());
-        }
+        F3S_TRY(launch_pass<false>(row_ptr, col_idx, n, nnz, W, counts, nullptr, nullptr,
+                                   nullptr, hubs, num_hubs, err, stream));
         int64_t* offs64 = reinterpret_cast<int64_t*>(s.offs64.ptr);
         F3S_TRY(exclusive_scan_i32_to_i64(counts, offs64, W,
                                           reinterpret_cast<int64_t*>(s.tmp.ptr), stream));
@@ -424,12 +940,8 @@ static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, i
         return F3S_OK;
     }
 
-    if (W > 0) {
-        hipLaunchKernelGGL((convert_windows<true>), dim3(W), dim3(kConvThreads), 0, stream,
-                           row_ptr, col_idx, n, nnz, W, nullptr, window_offsets, block_col,
-                           tile_mask, err);
-        F3S_HIP(hipGetLastError());
-    }
+    F3S_TRY(launch_pass<true>(row_ptr, col_idx, n, nnz, W, nullptr, window_offsets, block_col,
+                              tile_mask, hubs, num_hubs, err, stream));
     int32_t h_err = 0, total = 0;
     F3S_HIP(hipMemcpyAsync(&h_err, err, sizeof h_err, hipMemcpyDeviceToHost, stream));
     F3S_HIP(hipMemcpyAsync(&total, window_offsets + W, sizeof total, hipMemcpyDeviceToHost,

@@ -10,6 +10,18 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also fences
+// global memory, which makes every wave wait for all of its outstanding
+// vector-memory loads (s_waitcnt vmcnt(0)) at each barrier; this one waits
+// for LDS operations only, so loads issued ahead of time stay in flight.
+// Global stores made before it are NOT visible to the other waves after it.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Inclusive scan over the 64 lanes of a wave.
 template <typename T>
 __device__ __forceinline__ T wave_inclusive_scan(T v)

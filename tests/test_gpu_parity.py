@@ -181,8 +181,9 @@ def test_converter_hub_windows(gpu):
 
 
 def test_converter_column_slices(gpu):
-    # more block columns than one LDS bitmap slice (131072): windows with edges
-    # in both slices, and a last slice whose word count is not a multiple of 4
+    # more block columns than one 65,536-column slice of the per-window
+    # kernel's bitmap (hub windows sweep slices): windows with edges in both
+    # slices, and a last slice whose word count is not a multiple of 4
     n = 2_200_000
     r = rng(11)
     deg = r.integers(0, 4, n)
@@ -192,6 +193,22 @@ def test_converter_column_slices(gpu):
     ci = r.integers(0, n, int(rp[-1])).astype(np.int32)
     ci[rp[:2000]] = n - 1 - r.integers(0, 40, 2000)   # far end of the last slice
     ci[rp[:2000] + 1] = r.integers(0, 16 * 131072, 2000)
+    check_converter(gpu, rp.astype(np.int32), ci)
+
+
+@pytest.mark.parametrize("n", [4_194_304, 4_194_320])
+def test_converter_bitmap_limit(gpu, n):
+    # 4,194,304 nodes = 262,144 block columns: the widest graph whose block
+    # columns fit the persistent kernel's LDS bitmap (8,192 words); one more
+    # window sends every window through the per-window kernel instead.
+    # Hub rows (> 1,024 edges per window) exercise the hub launch as well.
+    r = rng(12)
+    deg = r.integers(0, 3, n)
+    deg[:64] += 200                      # four hub windows
+    rp = np.zeros(n + 1, np.int64)
+    rp[1:] = np.cumsum(deg)
+    ci = r.integers(0, n, int(rp[-1])).astype(np.int32)
+    ci[rp[:64]] = n - 1                  # last block column
     check_converter(gpu, rp.astype(np.int32), ci)
 
 
