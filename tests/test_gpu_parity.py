@@ -181,9 +181,9 @@ def test_converter_hub_windows(gpu):
 
 
 def test_converter_column_slices(gpu):
-    # more block columns than one 65,536-column slice of the per-window
-    # kernel's bitmap (hub windows sweep slices): windows with edges in both
-    # slices, and a last slice whose word count is not a multiple of 4
+    # 137,500 block columns: one 4,297-word bitmap in the persistent kernel
+    # (more than the per-window kernel's 65,536-column slice), windows with
+    # edges at both ends of the column range
     n = 2_200_000
     r = rng(11)
     deg = r.integers(0, 4, n)
