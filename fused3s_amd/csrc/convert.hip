@@ -53,11 +53,12 @@ static_assert(kSumWords == kWave, "the summary is scanned by one wave");
 enum ConvErr : int32_t { kErrNone = 0, kErrRowPtr = 1, kErrCol = 2, kErrCount = 4 };
 
 // The count pass needs only the bitmap; its LDS stays small for occupancy.
-template <bool FILL>
+// MT tile masks are staged at once (one per thread of the workgroup).
+template <bool FILL, int MT>
 struct ConvLds {
     uint32_t bits[kBitWords];                  // block columns of the current slice
     uint32_t base[FILL ? kBitWords : 1];       // tiles before each non-empty word
-    uint32_t masks[FILL ? kMaskTiles * 8 : 1]; // row masks of tiles [ms, ms + kMaskTiles)
+    uint32_t masks[FILL ? MT * 8 : 1];         // row masks of tiles [ms, ms + MT)
     uint16_t list[FILL ? kBitWords : 2];       // non-empty words, ascending
     uint32_t summary[FILL ? kSumWords : 1];    // non-empty bitmap words
     uint32_t slices[kMaxSlices / 32];          // slices holding at least one edge
@@ -109,7 +110,7 @@ __device__ __forceinline__ int row_of_edge(const int32_t* rp, int nrows, int32_t
 // against the offsets.
 template <bool FILL, int NT>
 __device__ __forceinline__ void
-convert_one_window(ConvLds<FILL>& L, int32_t w, const int32_t* __restrict__ row_ptr,
+convert_one_window(ConvLds<FILL, NT>& L, int32_t w, const int32_t* __restrict__ row_ptr,
                    const int32_t* __restrict__ col_idx, int32_t n, int64_t nnz, int32_t W,
                    int32_t* __restrict__ counts, const int32_t* __restrict__ window_offsets,
                    int32_t* __restrict__ block_col, uint16_t* __restrict__ tile_mask,
@@ -330,9 +331,9 @@ convert_one_window(ConvLds<FILL>& L, int32_t w, const int32_t* __restrict__ row_
                     }
                     __syncthreads();
                 }
-                // ---- tile masks, kMaskTiles at a time ----
-                for (int32_t ms = 0; in_regs && ms < total; ms += kMaskTiles) {
-                    for (int i = tid; i < kMaskTiles * 2; i += NT)
+                // ---- tile masks, NT at a time ----
+                for (int32_t ms = 0; in_regs && ms < total; ms += NT) {
+                    for (int i = tid; i < NT * 2; i += NT)
                         *reinterpret_cast<uint4*>(&L.masks[4 * i]) = make_uint4(0u, 0u, 0u, 0u);
                     __syncthreads();
                     int32_t cur = -1;
@@ -344,7 +345,7 @@ convert_one_window(ConvLds<FILL>& L, int32_t w, const int32_t* __restrict__ row_
                         const uint32_t below = (1u << (q & 31)) - 1u;
                         const int32_t t2 =
                             (int32_t)(L.base[wi] + __popc(L.bits[wi] & below)) - ms;
-                        if (t2 < 0 || t2 >= kMaskTiles) return;
+                        if (t2 < 0 || t2 >= NT) return;
                         const int32_t idx = t2 * 8 + (r >> 1);
                         if (idx != cur) {
                             if (cur >= 0) atomicOr(&L.masks[cur], acc);
@@ -356,7 +357,7 @@ convert_one_window(ConvLds<FILL>& L, int32_t w, const int32_t* __restrict__ row_
                     if (cur >= 0) atomicOr(&L.masks[cur], acc);
                     __syncthreads();
                     if (tile_mask) {
-                        const int32_t nt = min(kMaskTiles, total - ms);
+                        const int32_t nt = min(NT, total - ms);
                         for (int t3 = tid; t3 < nt; t3 += NT) {
                             const uint4* src = reinterpret_cast<const uint4*>(&L.masks[t3 * 8]);
                             uint4* dst = reinterpret_cast<uint4*>(
@@ -399,7 +400,7 @@ convert_hubs(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ co
              uint16_t* __restrict__ tile_mask, const int32_t* __restrict__ hubs,
              const int32_t* __restrict__ num_hubs, int32_t* __restrict__ err)
 {
-    __shared__ ConvLds<FILL> L;
+    __shared__ ConvLds<FILL, NT> L;
     const int32_t nh = hubs ? *num_hubs : W;
     for (int32_t i = blockIdx.x; i < nh; i += gridDim.x) {
         const int32_t w = hubs ? hubs[i] : i;
