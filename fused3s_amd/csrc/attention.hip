@@ -102,6 +102,7 @@ fused_attention_kernel(const AttnParams p)
 
     // ---- item decode (wave-uniform) ----
     int32_t w, tb, te, slot;
+    int32_t team_n = 1;   // teams: non-empty parts of the window (uniform over the team)
     if (p.items) {
         const Item it = p.items[item_idx];
         w = it.w;
@@ -109,6 +110,12 @@ fused_attention_kernel(const AttnParams p)
         te = it.te;
         slot = it.slot;
         if (w < 0 || w >= p.W) return;   // an invalid order entry (a whole team's items)
+        if constexpr (TEAM > 1) {
+            // the window's tiles run from its first part's start to its last
+            // part's end
+            const int64_t ib = item_idx - wave;
+            team_n = team_parts(p.items[ib].tb, p.items[ib + TEAM - 1].te, TEAM);
+        }
     } else {
         const int64_t wi = item_idx / TEAM;
         w = p.window_order ? p.window_order[wi] : (int32_t)wi;
@@ -124,12 +131,15 @@ fused_attention_kernel(const AttnParams p)
             if (heavy != (p.heavy_mode == 2)) return;
         }
         if constexpr (TEAM > 1) {
+            team_n = team_parts(tb, te, TEAM);
             const int32_t a = team_part(tb, te, wave, TEAM), b = team_part(tb, te, wave + 1, TEAM);
             tb = a;
             te = b;
         }
         slot = -1;
     }
+    // a window of at most one part is wave 0's alone: no merge, no barrier
+    if (TEAM > 1 && team_n <= 1 && wave != 0) return;
     const int32_t nbc = (n + 15) >> 4;   // valid block columns
     const int32_t* __restrict__ block_col = p.block_col;
     const __amdgpu_buffer_rsrc_t qres = make_rsrc(p.Q, p.feat_bytes);
@@ -305,12 +315,13 @@ fused_attention_kernel(const AttnParams p)
         }
     }
 
-    if constexpr (TEAM > 1) {
-        // ---- team merge: waves 1.. publish (m, l, O^T) lane by lane in their
-        // own LDS area, wave 0 folds them in, in wave order (deterministic) ----
+    if (TEAM > 1 && team_n > 1) {   // uniform over the team
+        // ---- team merge: waves 1 .. team_n-1 publish (m, l, O^T) lane by
+        // lane in their own LDS area, wave 0 folds them in, in wave order
+        // (deterministic) ----
         F3S_WAVE_LDS_SYNC();   // this wave's last reads of its stage are done
         float* accs = reinterpret_cast<float*>(L.stage);   // [t][lane][4]: 4 KB of 4.5
-        if (wave != 0) {
+        if (wave != 0 && wave < team_n) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) *reinterpret_cast<f4*>(&accs[(t * kWave + lane) * 4]) = st.acc[t];
             L.off[lane] = __float_as_uint(st.m);
@@ -320,7 +331,8 @@ fused_attention_kernel(const AttnParams p)
         if (wave != 0) return;
         float M = st.m;
 #pragma unroll
-        for (int k = 1; k < TEAM; ++k) M = __builtin_fmaxf(M, __uint_as_float(lds_all[k].off[lane]));
+        for (int k = 1; k < TEAM; ++k)
+            if (k < team_n) M = __builtin_fmaxf(M, __uint_as_float(lds_all[k].off[lane]));
         if (M != -INFINITY) {   // else no part of the team attended row r: all zero
             const float c0 = fast_exp2(st.m - M);   // 0 when this part is empty
             st.l *= c0;
@@ -328,6 +340,7 @@ fused_attention_kernel(const AttnParams p)
             for (int t = 0; t < 4; ++t) st.acc[t] *= c0;
 #pragma unroll
             for (int k = 1; k < TEAM; ++k) {
+                if (k >= team_n) break;
                 const float mk = __uint_as_float(lds_all[k].off[lane]);
                 const float f = fast_exp2(mk - M);   // mk = -inf: 0
                 st.l += __uint_as_float(lds_all[k].rm[lane]) * f;

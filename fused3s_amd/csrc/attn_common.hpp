@@ -90,12 +90,22 @@ __host__ __device__ __forceinline__ int32_t heavy_tiles(int32_t T, int32_t W)
 // wave taking an even share of the window's tiles (cut at tile pairs, the
 // tile-dense chunk), and the team merges its (m, l, O) states through LDS, so
 // the heaviest window no longer runs as one wave's serial chain and no merge
-// launch is needed.  Part k of a window's tiles [tb, te):
+// launch is needed.  A window of fewer tile pairs than waves has only as many
+// parts, on waves 0.. (the others have nothing to do and publish nothing).
+// Number of non-empty parts of [tb, te):
+__host__ __device__ __forceinline__ int32_t team_parts(int32_t tb, int32_t te, int32_t team)
+{
+    const int64_t pairs = ((int64_t)te - tb + 1) / 2;
+    return (int32_t)(pairs < team ? pairs : team);
+}
+// Start of part k of a window's tiles [tb, te) (part k = [part(k), part(k + 1))):
 __host__ __device__ __forceinline__ int32_t team_part(int32_t tb, int32_t te, int32_t k,
                                                       int32_t team)
 {
     const int64_t pairs = ((int64_t)te - tb + 1) / 2;
-    const int64_t a = tb + 2 * ((pairs * k) / team);
+    const int64_t parts = pairs < team ? pairs : team;
+    if (k >= parts) return te;
+    const int64_t a = tb + 2 * ((pairs * k) / parts);
     return (int32_t)(a < te ? a : te);
 }
 constexpr int kTeamSmall = 4;
