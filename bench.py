@@ -8,8 +8,10 @@ pass over the whole graph with inputs already resident in HBM.
 
 Prints one JSON line: whole-job edges/s over K timed steps, the roofline
 of the fused kernel (algorithmic bytes / average launch time measured with
-HIP events on the launch stream) and the reference's own CPU baseline
-(baselines/cpu_baseline.cpp, compiled under oracle/_ref) timed on this host.
+HIP events on the launch stream), the reference's own CPU baseline
+(baselines/cpu_baseline.cpp, compiled under oracle/_ref, one thread as in
+the reference) and the CPU restatement of it on all available host cores
+(OpenMP, at most 16), both timed on this host.
 """
 from __future__ import annotations
 
@@ -101,6 +103,33 @@ def cpu_baseline(rp, ci, Q, K, V, n: int, d: int) -> dict | None:
     return {"value": edges / dt, "unit": "edges/s", "cores": 1, "kind": kind,
             "sample": f"all {n} rows / {edges} edges of the workload, one call, "
                       f"{dt:.2f} s on {os.cpu_count()} visible host cores (1 used)"}
+
+
+def cpu_baseline_all_cores(rp, ci, Q, K, V, n: int, H: int, d: int) -> dict | None:
+    """The CPU restatement of cpu_sparse_attention_csr (oracle/f3s_oracle.c,
+    OpenMP over rows) on the host cores this process may use, at most 16 (a
+    one-GPU box's CPU share), over the whole graph and every head."""
+    lib_path = ROOT / "oracle" / "liboracle.so"
+    if not lib_path.exists():
+        return None
+    lib = C.CDLL(str(lib_path))
+    fn = lib.orc_masked_attention
+    fn.restype = None
+    fn.argtypes = ([C.c_int32] * 3 + [C.c_void_p] * 5 + [C.c_float, C.c_int32, C.c_int32,
+                                                         C.c_void_p, C.c_int32])
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    Qf, Kf, Vf = (np.ascontiguousarray(x.reshape(n, H, d), np.float32) for x in (Q, K, V))
+    rp32 = np.ascontiguousarray(rp, np.int32)
+    ci32 = np.ascontiguousarray(ci, np.int32)
+    O = np.zeros((n, H, d), np.float32)
+    t0 = time.perf_counter()
+    fn(n, d, H, Qf.ctypes.data, Kf.ctypes.data, Vf.ctypes.data, rp32.ctypes.data,
+       ci32.ctypes.data, 1.0, 0, n, O.ctypes.data, threads)
+    dt = time.perf_counter() - t0
+    edges = int(rp[n])
+    return {"value": edges / dt, "unit": "edges/s", "cores": threads, "kind": "port",
+            "sample": f"all {n} rows / {edges} edges x {H} head(s), one call, {dt:.2f} s on "
+                      f"{threads} threads (OpenMP) of {len(os.sched_getaffinity(0))} available cores"}
 
 
 def main() -> int:
@@ -255,6 +284,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
         "cpu_baseline": None,
+        "cpu_baseline_all_cores": None,
         "kernel_us": {"mean": kavg * 1e3, "min": float(kern_ms.min()) * 1e3,
                       "median": float(np.median(kern_ms)) * 1e3, "cold_first_launch": cold_ms * 1e3},
         "alg_bytes_per_launch": nbytes,
@@ -270,6 +300,9 @@ def main() -> int:
         print("[bench] timing the reference CPU baseline ...", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(rp, ci, Q.astype(np.float32), K.astype(np.float32),
                                            V.astype(np.float32), n, d) if H == 1 else None
+        print("[bench] timing the CPU restatement on all available cores ...", file=sys.stderr,
+              flush=True)
+        res["cpu_baseline_all_cores"] = cpu_baseline_all_cores(rp, ci, Q, K, V, n, H, d)
     print(json.dumps(res), flush=True)
     return 0
 
