@@ -123,11 +123,15 @@ fused_attention_kernel(const AttnParams p)
         const int32_t T = p.window_offsets[p.W];
         tb = max(0, min(p.window_offsets[w], T));
         te = max(tb, min(p.window_offsets[w + 1], T));
-        if (p.heavy_mode) {
+        if (p.heavy_mode == 3) {
+            // natural order: the listed heavy windows belong to the team launch
+            if ((p.heavy_listed[w >> 5] >> (w & 31)) & 1u) return;
+        } else if (p.heavy_mode) {
             // the heavy windows among the first heavy_max order positions
             // belong to the team launch (mode 2), all others to the one-wave
             // launch (mode 1); uniform over a team's workgroup
-            const bool heavy = wi < p.heavy_max && te - tb > heavy_tiles(T, p.W);
+            const bool heavy =
+                wi < p.heavy_max && te - tb > heavy_tiles(T, p.W, p.heavy_min, p.heavy_factor);
             if (heavy != (p.heavy_mode == 2)) return;
         }
         if constexpr (TEAM > 1) {
@@ -719,6 +723,74 @@ static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
         launch_mw<MODE, false>(p, waves, st);
 }
 
+// Natural-order unplanned launches: the first kHeavyMaxWindowsNat heavy
+// windows in window order (deterministic), as a window order for the team
+// launch (entries past the count stay -1, which that launch skips) and as a
+// bitmap the one-wave launch skips.  Blocks of 256 windows cover whole bitmap
+// words.  heavy_count: per block, the number of its heavy windows; zeroes the
+// block's bitmap words; block 0 fills the list with -1.
+__global__ void __launch_bounds__(256)
+heavy_count(const int32_t* __restrict__ window_offsets, int32_t W, int32_t* __restrict__ list,
+            int32_t* __restrict__ block_counts, uint32_t* __restrict__ listed)
+{
+    const int32_t w = blockIdx.x * 256 + threadIdx.x;
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < kHeavyMaxWindowsNat; i += 256) list[i] = -1;
+    if (threadIdx.x < 8 && (int64_t)blockIdx.x * 8 + threadIdx.x < ((int64_t)W + 31) / 32)
+        listed[blockIdx.x * 8 + threadIdx.x] = 0u;
+    const int32_t T = window_offsets[W];
+    bool heavy = false;
+    if (w < W) {
+        const int32_t tb = max(0, min(window_offsets[w], T));
+        const int32_t te = max(tb, min(window_offsets[w + 1], T));
+        heavy = te - tb > heavy_tiles(T, W, kHeavyMinTilesNat, kHeavyMeanFactorNat);
+    }
+    __shared__ int32_t wc[4];
+    const int32_t c = __popcll(__ballot(heavy));
+    if ((threadIdx.x & (kWave - 1)) == 0) wc[threadIdx.x / kWave] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) block_counts[blockIdx.x] = wc[0] + wc[1] + wc[2] + wc[3];
+}
+
+// heavy_list: a heavy window's rank is the heavy windows of earlier blocks
+// plus those before it in its block; ranks below kHeavyMaxWindowsNat are listed.
+__global__ void __launch_bounds__(256)
+heavy_list(const int32_t* __restrict__ window_offsets, int32_t W,
+           const int32_t* __restrict__ block_counts, int32_t* __restrict__ list,
+           uint32_t* __restrict__ listed)
+{
+    __shared__ int32_t red[4];
+    __shared__ int32_t wc[4];
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    int32_t before = 0;
+    for (int32_t b = threadIdx.x; b < (int32_t)blockIdx.x; b += 256) before += block_counts[b];
+    before = wave_sum(before);
+    if (lane == 0) red[wid] = before;
+    __syncthreads();
+    before = red[0] + red[1] + red[2] + red[3];
+    if (before >= kHeavyMaxWindowsNat) return;   // uniform
+    const int32_t w = blockIdx.x * 256 + threadIdx.x;
+    const int32_t T = window_offsets[W];
+    bool heavy = false;
+    if (w < W) {
+        const int32_t tb = max(0, min(window_offsets[w], T));
+        const int32_t te = max(tb, min(window_offsets[w + 1], T));
+        heavy = te - tb > heavy_tiles(T, W, kHeavyMinTilesNat, kHeavyMeanFactorNat);
+    }
+    const uint64_t bal = __ballot(heavy);
+    if (lane == 0) wc[wid] = __popcll(bal);
+    __syncthreads();
+    int32_t rank = before + __popcll(bal & ((1ull << lane) - 1ull));
+    for (int v = 0; v < wid; ++v) rank += wc[v];
+    const bool take = heavy && rank < kHeavyMaxWindowsNat;
+    if (take) list[rank] = w;
+    // each wave writes its two bitmap words
+    const uint64_t tb = __ballot(take);
+    const int64_t word = ((int64_t)blockIdx.x * 256 + wid * kWave) / 32;
+    if (lane == 0 && word < ((int64_t)W + 31) / 32) listed[word] = (uint32_t)tb;
+    if (lane == 1 && word + 1 < ((int64_t)W + 31) / 32) listed[word + 1] = (uint32_t)(tb >> 32);
+}
+
 static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
 {
     if (p.num_items <= 0) return F3S_OK;
@@ -778,6 +850,51 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
     p.n = n;
     p.xcd_contiguous = d_window_order == nullptr;
     hipStream_t st = as_stream(stream);
+    if (p.team == 1 && !d_window_order && !wide_features(n, H) && W > kHeavyMaxWindows) {
+        // Natural order: the hubs can be anywhere.  Two small kernels list the
+        // first kHeavyMaxWindowsNat heavy windows (tens of KB of stream-ordered
+        // scratch); teams of 16 waves take those, one wave each takes the rest.
+        const int32_t nb = (int32_t)ceil_div(W, 256);
+        const size_t words = (size_t)ceil_div(W, 32);
+        const size_t bytes = sizeof(int32_t) * ((size_t)kHeavyMaxWindowsNat + nb) +
+                             sizeof(uint32_t) * words;
+        void* scratch = nullptr;
+        if (hipMallocAsync(&scratch, bytes, st) != hipSuccess) {
+            (void)hipGetLastError();   // no stream-ordered pool: one launch as before
+            return launch(p, H, scale, st);
+        }
+        int32_t* list = reinterpret_cast<int32_t*>(scratch);
+        int32_t* counts = list + kHeavyMaxWindowsNat;
+        uint32_t* listed = reinterpret_cast<uint32_t*>(counts + nb);
+        hipLaunchKernelGGL(heavy_count, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
+                           list, counts, listed);
+        hipLaunchKernelGGL(heavy_list, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
+                           counts, list, listed);
+        const hipError_t le = hipGetLastError();
+        f3s_status s =
+            le == hipSuccess ? F3S_OK : hip_fail(le, "heavy window list", __FILE__, __LINE__);
+        if (s == F3S_OK) {
+            AttnParams ph = p;
+            ph.window_order = list;
+            ph.xcd_contiguous = 0;
+            ph.team = kTeamLarge;
+            ph.num_items = (int64_t)kHeavyMaxWindowsNat * kTeamLarge;
+            ph.heavy_mode = 2;
+            ph.heavy_max = kHeavyMaxWindowsNat;
+            ph.heavy_min = kHeavyMinTilesNat;
+            ph.heavy_factor = kHeavyMeanFactorNat;
+            s = launch(ph, H, scale, st);
+        }
+        if (s == F3S_OK) {
+            p.heavy_mode = 3;
+            p.heavy_listed = listed;
+            s = launch(p, H, scale, st);
+        }
+        const hipError_t fe = hipFreeAsync(scratch, st);   // after the launches, in stream order
+        if (s != F3S_OK) return s;
+        F3S_HIP(fe);
+        return F3S_OK;
+    }
     if (p.team == 1 && d_window_order && !wide_features(n, H)) {
         // Without a plan a hub window would run on one wave.  Given a window
         // order, two launches instead: teams of 16 waves for the heavy
@@ -792,9 +909,13 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
         ph.num_items = (int64_t)K * kTeamLarge;
         ph.heavy_mode = 2;
         ph.heavy_max = K;
+        ph.heavy_min = kHeavyMinTiles;
+        ph.heavy_factor = kHeavyMeanFactor;
         F3S_TRY(launch(ph, H, scale, st));
         p.heavy_mode = 1;
         p.heavy_max = K;
+        p.heavy_min = kHeavyMinTiles;
+        p.heavy_factor = kHeavyMeanFactor;
     }
     return launch(p, H, scale, st);
 }

@@ -70,20 +70,33 @@ struct AttnParams {
     int32_t team;                    // waves per window (1, or kTeamSmall / kTeamLarge)
     int32_t heavy_mode;              // unplanned launches: 0 all windows; 1 all but the heavy
                                      // windows among the first heavy_max order positions;
-                                     // 2 only those (teams)
+                                     // 2 only those (teams); 3 all but the windows set in
+                                     // heavy_listed (natural order)
     int32_t heavy_max;
+    int32_t heavy_min, heavy_factor; // heavy: more tiles than max(heavy_min, heavy_factor x mean)
+    const uint32_t* heavy_listed;    // heavy_mode 3: bitmap of the windows a team launch took
 };
 
 // A window is heavy for the unplanned two-launch schedule when its tiles
-// exceed both kHeavyMinTiles and kHeavyMeanFactor times the mean window.
+// exceed both a minimum and a multiple of the mean window: given a window
+// order, kHeavyMinTiles and kHeavyMeanFactor, and only the first
+// kHeavyMaxWindows order positions (the reference's descending order puts the
+// hubs there and runs the other windows big-first); in natural order, where
+// a window just under the threshold may start last, the lower
+// kHeavyMinTilesNat and kHeavyMeanFactorNat, and the first
+// kHeavyMaxWindowsNat heavy windows by index.
 constexpr int32_t kHeavyMinTiles = 1024;
 constexpr int32_t kHeavyMeanFactor = 8;
-constexpr int32_t kHeavyMaxWindows = 512;   // order positions the team launch covers
-__host__ __device__ __forceinline__ int32_t heavy_tiles(int32_t T, int32_t W)
+constexpr int32_t kHeavyMaxWindows = 512;
+constexpr int32_t kHeavyMinTilesNat = 512;
+constexpr int32_t kHeavyMeanFactorNat = 2;
+constexpr int32_t kHeavyMaxWindowsNat = 4096;
+__host__ __device__ __forceinline__ int32_t heavy_tiles(int32_t T, int32_t W, int32_t min_tiles,
+                                                        int32_t factor)
 {
     const int64_t mean = W > 0 ? ((int64_t)T + W - 1) / W : 0;
-    const int64_t thr = mean * kHeavyMeanFactor;
-    return (int32_t)(thr > kHeavyMinTiles ? thr : kHeavyMinTiles);
+    const int64_t thr = mean * factor;
+    return (int32_t)(thr > min_tiles ? thr : min_tiles);
 }
 
 // Small graphs: a team of waves in one workgroup shares each row window, each

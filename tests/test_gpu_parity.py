@@ -490,12 +490,12 @@ def test_concurrent_streams_and_threads(gpu):
 
 
 def test_unplanned_heavy_windows(gpu):
-    # Without a plan but with a window order, windows of more than
-    # max(1024, 8 x mean) tiles among the first 512 order positions run as
-    # 16-wave teams in a launch of their own; every other window runs on one
-    # wave in the second launch (and all do in natural order).  Hubs sit in
-    # windows 0, 1 and 562 (1,250 tiles each); the orders put them first
-    # (sorted) or at positions 700, 5 and 100 (one of them past 512).
+    # Without a plan, windows of more than max(1024, 8 x mean) tiles run as
+    # 16-wave teams in a launch of their own -- given a window order, those
+    # among its first 512 positions; in natural order, the first 512 heavy
+    # windows by index -- and every other window on one wave in a second
+    # launch.  Hubs sit in windows 0, 1 and 562 (1,250 tiles each); the orders
+    # put them first (sorted) or at positions 700, 5 and 100 (one past 512).
     rp, ci = star_graph(20000, hubs=(0, 3, 17, 9000))
     p = Problem(gpu, rp, ci, H=2, normal=True, seed=61)
     W = p.bsf.W
@@ -512,9 +512,51 @@ def test_unplanned_heavy_windows(gpu):
               "moved": gpu.DeviceArray.from_numpy(perm)}
     for masked in (True, False):
         want = p.oracle(masked, scale=0.125)
+        got_by = {}
         for name, order in orders.items():
             got = p.run(masked, order=order, scale=0.125)
             assert_close(got, want, f"unplanned heavy windows masked={masked} order={name}")
+            got_by[name] = got
+        # natural and sorted orders give all three hubs to teams: same bits
+        assert np.array_equal(got_by["natural"].view(np.uint32), got_by["sorted"].view(np.uint32))
+
+
+def test_unplanned_natural_order_heavy_cap(gpu):
+    # Natural order counts a window as heavy above max(512, 2 x mean) tiles
+    # and gives the first 4,096 of them by index to the team launch.  Here
+    # 4,200 windows (every 4th of 16,800) hold exactly 600 tiles: the last
+    # 104 run on one wave each, and the listing kernels' 256-window blocks
+    # each hold 64 of them.  With a window order the rule is max(1024,
+    # 8 x mean) = 1,208 tiles, so no window is heavy there.  Results meet the
+    # oracle; repeated runs give the same bits.
+    W = 16_800
+    n = 16 * W
+    heavy_w = np.arange(4200) * 4
+    rows, cols = [np.arange(n)], [np.arange(n)]            # self-loops
+    k = np.arange(600, dtype=np.int64)
+    for w in heavy_w:
+        rows.append(np.full(600, 16 * w))
+        cols.append(16 * ((k * 7919 + w) % W) + (w % 16))   # 600 distinct block columns
+    e = np.unique(np.stack([np.concatenate(rows), np.concatenate(cols)], 1), axis=0)
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, e[:, 0] + 1, 1)
+    rp = np.cumsum(rp).astype(np.int32)
+    ci = e[:, 1].astype(np.int32)
+    p = Problem(gpu, rp, ci, H=2, normal=True, seed=63)
+    offs = p.bsf.window_offsets.numpy()
+    tiles = np.diff(offs)
+    mean = (int(offs[-1]) + W - 1) // W
+    assert np.array_equal(np.nonzero(tiles > max(512, 2 * mean))[0], heavy_w)
+    assert not np.any(tiles > max(1024, 8 * mean))
+    sorted_order = gpu.window_order_device(p.bsf)
+    for masked in (True, False):
+        want = p.oracle(masked)
+        a = p.run(masked)
+        b = p.run(masked)
+        s = p.run(masked, order=sorted_order)
+        assert_close(a, want, f"natural order, 4,200 heavy windows, masked={masked}")
+        assert_close(s, want, f"sorted order, masked={masked}")
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 @pytest.mark.parametrize("H", [1, 16])
