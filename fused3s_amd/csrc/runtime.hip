@@ -230,7 +230,12 @@ f3s_status f3s_device_name(char* buf, int32_t buflen)
     F3S_HIP(hipGetDevice(&dev));
     hipDeviceProp_t p;
     F3S_HIP(hipGetDeviceProperties(&p, dev));
-    snprintf(buf, (size_t)buflen, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    // some drivers leave the marketing name empty: then the architecture alone
+    if (p.name[0])
+        snprintf(buf, (size_t)buflen, "%s (%s, %d CUs)", p.name, p.gcnArchName,
+                 p.multiProcessorCount);
+    else
+        snprintf(buf, (size_t)buflen, "%s, %d CUs", p.gcnArchName, p.multiProcessorCount);
     return F3S_OK;
 }
 
