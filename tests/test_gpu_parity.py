@@ -489,6 +489,45 @@ def test_concurrent_streams_and_threads(gpu):
         assert np.array_equal(outs[k].view(np.uint32), want.view(np.uint32))
 
 
+def test_concurrent_converter_and_natural_order_launch(gpu):
+    # Two host threads, each with its own stream, convert their own graph and
+    # run unplanned natural-order passes (whose heavy-window list lives in
+    # stream-ordered scratch) at the same time; every result equals a
+    # single-threaded run, and each thread's tile lists match the oracle.
+    import threading
+    graphs = [star_graph(20000, hubs=(0, 3, 17, 9000)), star_graph(24000, hubs=(5, 12000))]
+    probs = [Problem(gpu, rp, ci, H=1, normal=True, seed=71 + k) for k, (rp, ci) in enumerate(graphs)]
+    wants = [p.run(True) for p in probs]
+    results, errs = {}, []
+
+    def worker(k):
+        try:
+            p = probs[k]
+            st = gpu.Stream()
+            bsf = gpu.convert_device(gpu.DeviceCSR(p.rp, p.ci, st), stream=st)
+            dO = gpu.DeviceArray((p.n, 1, 64), np.float32)
+            for _ in range(5):
+                gpu.attention_fwd(p.dQ, p.dK, p.dV, dO, bsf, None, masked=True, H=1, stream=st)
+            st.synchronize()
+            results[k] = (bsf.to_host(), dO.numpy())
+        except Exception as e:   # surfaced in the main thread
+            errs.append(e)
+
+    th = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join(timeout=120)
+    assert not errs, errs
+    for k, p in enumerate(probs):
+        hb, out = results[k]
+        offs, bcol, mask = orc.convert(p.n, p.rp, p.ci)
+        assert np.array_equal(hb.window_offsets, offs)
+        assert np.array_equal(hb.block_col_indices, bcol)
+        assert np.array_equal(hb.tile_masks, mask)
+        assert np.array_equal(out.view(np.uint32), wants[k].view(np.uint32))
+
+
 def test_unplanned_heavy_windows(gpu):
     # Without a plan, windows of more than max(1024, 8 x mean) tiles run as
     # 16-wave teams in a launch of their own -- given a window order, those
