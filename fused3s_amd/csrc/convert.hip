@@ -433,8 +433,9 @@ convert_hubs(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ co
 //          block columns and masks leave in coalesced stores;
 //   clear  every edge clears its bitmap word.
 // The per-edge work is a handful of VALU operations and one or two LDS
-// atomics: the pass is bound by instruction issue, so it keeps no per-edge
-// state beyond the column (and, filling, the row).  Windows with more edges
+// atomics: the passes are bound by instruction issue, and the fill pass also
+// by the occupancy its LDS allows, so they keep no per-edge state beyond the
+// column (and, filling, the row) and stage no more than kMaskTiles tiles.  Windows with more edges
 // are listed for convert_hubs, so that one heavy window never holds up the
 // windows queued behind it in this workgroup.
 // ---------------------------------------------------------------------------
