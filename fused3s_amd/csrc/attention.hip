@@ -723,28 +723,44 @@ static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
         launch_mw<MODE, false>(p, waves, st);
 }
 
-// Natural-order unplanned launches: the first kHeavyMaxWindowsNat heavy
-// windows in window order (deterministic), as a window order for the team
-// launch (entries past the count stay -1, which that launch skips) and as a
-// bitmap the one-wave launch skips.  Blocks of 256 windows cover whole bitmap
-// words.  heavy_count: per block, the number of its heavy windows; zeroes the
-// block's bitmap words; block 0 fills the list with -1.
+// Natural-order unplanned launches: the heavy windows of a class (more tiles
+// than the class threshold and, for the medium class, no more than the large
+// threshold), the first `cap` of them by index (deterministic), as a window
+// order for a team launch (entries past the count stay -1, which that launch
+// skips) and as bits of a bitmap the one-wave launch skips.  Blocks of 256
+// windows cover whole bitmap words.
+struct HeavyClass {
+    int32_t lo_min, lo_factor;   // in the class: more tiles than max(lo_min, lo_factor x mean)
+    int32_t hi_min, hi_factor;   // ... and, if hi_min > 0, no more than max(hi_min, hi_factor x mean)
+    int32_t cap;                 // list entries
+};
+
+__device__ __forceinline__ bool heavy_in_class(const int32_t* __restrict__ window_offsets,
+                                               int32_t W, int32_t w, const HeavyClass& hc)
+{
+    if (w >= W) return false;
+    const int32_t T = window_offsets[W];
+    const int32_t tb = max(0, min(window_offsets[w], T));
+    const int32_t te = max(tb, min(window_offsets[w + 1], T));
+    const int32_t t = te - tb;
+    return t > heavy_tiles(T, W, hc.lo_min, hc.lo_factor) &&
+           (hc.hi_min <= 0 || t <= heavy_tiles(T, W, hc.hi_min, hc.hi_factor));
+}
+
+// heavy_count: per block, the number of its windows in the class; block 0
+// fills the list with -1; `zero_bits` also zeroes the block's bitmap words.
 __global__ void __launch_bounds__(256)
-heavy_count(const int32_t* __restrict__ window_offsets, int32_t W, int32_t* __restrict__ list,
-            int32_t* __restrict__ block_counts, uint32_t* __restrict__ listed)
+heavy_count(const int32_t* __restrict__ window_offsets, int32_t W, HeavyClass hc,
+            int32_t* __restrict__ list, int32_t* __restrict__ block_counts,
+            uint32_t* __restrict__ listed, int32_t zero_bits)
 {
     const int32_t w = blockIdx.x * 256 + threadIdx.x;
     if (blockIdx.x == 0)
-        for (int i = threadIdx.x; i < kHeavyMaxWindowsNat; i += 256) list[i] = -1;
-    if (threadIdx.x < 8 && (int64_t)blockIdx.x * 8 + threadIdx.x < ((int64_t)W + 31) / 32)
+        for (int i = threadIdx.x; i < hc.cap; i += 256) list[i] = -1;
+    if (zero_bits && threadIdx.x < 8 &&
+        (int64_t)blockIdx.x * 8 + threadIdx.x < ((int64_t)W + 31) / 32)
         listed[blockIdx.x * 8 + threadIdx.x] = 0u;
-    const int32_t T = window_offsets[W];
-    bool heavy = false;
-    if (w < W) {
-        const int32_t tb = max(0, min(window_offsets[w], T));
-        const int32_t te = max(tb, min(window_offsets[w + 1], T));
-        heavy = te - tb > heavy_tiles(T, W, kHeavyMinTilesNat, kHeavyMeanFactorNat);
-    }
+    const bool heavy = heavy_in_class(window_offsets, W, w, hc);
     __shared__ int32_t wc[4];
     const int32_t c = __popcll(__ballot(heavy));
     if ((threadIdx.x & (kWave - 1)) == 0) wc[threadIdx.x / kWave] = c;
@@ -752,10 +768,11 @@ heavy_count(const int32_t* __restrict__ window_offsets, int32_t W, int32_t* __re
     if (threadIdx.x == 0) block_counts[blockIdx.x] = wc[0] + wc[1] + wc[2] + wc[3];
 }
 
-// heavy_list: a heavy window's rank is the heavy windows of earlier blocks
-// plus those before it in its block; ranks below kHeavyMaxWindowsNat are listed.
+// heavy_list: a window's rank in its class is the class's windows in earlier
+// blocks plus those before it in its block; ranks below the cap are listed
+// and their bits ORed into the bitmap (one lane per word).
 __global__ void __launch_bounds__(256)
-heavy_list(const int32_t* __restrict__ window_offsets, int32_t W,
+heavy_list(const int32_t* __restrict__ window_offsets, int32_t W, HeavyClass hc,
            const int32_t* __restrict__ block_counts, int32_t* __restrict__ list,
            uint32_t* __restrict__ listed)
 {
@@ -768,27 +785,21 @@ heavy_list(const int32_t* __restrict__ window_offsets, int32_t W,
     if (lane == 0) red[wid] = before;
     __syncthreads();
     before = red[0] + red[1] + red[2] + red[3];
-    if (before >= kHeavyMaxWindowsNat) return;   // uniform
+    if (before >= hc.cap) return;   // uniform
     const int32_t w = blockIdx.x * 256 + threadIdx.x;
-    const int32_t T = window_offsets[W];
-    bool heavy = false;
-    if (w < W) {
-        const int32_t tb = max(0, min(window_offsets[w], T));
-        const int32_t te = max(tb, min(window_offsets[w + 1], T));
-        heavy = te - tb > heavy_tiles(T, W, kHeavyMinTilesNat, kHeavyMeanFactorNat);
-    }
+    const bool heavy = heavy_in_class(window_offsets, W, w, hc);
     const uint64_t bal = __ballot(heavy);
     if (lane == 0) wc[wid] = __popcll(bal);
     __syncthreads();
     int32_t rank = before + __popcll(bal & ((1ull << lane) - 1ull));
     for (int v = 0; v < wid; ++v) rank += wc[v];
-    const bool take = heavy && rank < kHeavyMaxWindowsNat;
+    const bool take = heavy && rank < hc.cap;
     if (take) list[rank] = w;
-    // each wave writes its two bitmap words
+    // each wave owns its two bitmap words
     const uint64_t tb = __ballot(take);
     const int64_t word = ((int64_t)blockIdx.x * 256 + wid * kWave) / 32;
-    if (lane == 0 && word < ((int64_t)W + 31) / 32) listed[word] = (uint32_t)tb;
-    if (lane == 1 && word + 1 < ((int64_t)W + 31) / 32) listed[word + 1] = (uint32_t)(tb >> 32);
+    if (lane == 0 && word < ((int64_t)W + 31) / 32) listed[word] |= (uint32_t)tb;
+    if (lane == 1 && word + 1 < ((int64_t)W + 31) / 32) listed[word + 1] |= (uint32_t)(tb >> 32);
 }
 
 static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
@@ -851,38 +862,50 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
     p.xcd_contiguous = d_window_order == nullptr;
     hipStream_t st = as_stream(stream);
     if (p.team == 1 && !d_window_order && !wide_features(n, H) && W > kHeavyMaxWindows) {
-        // Natural order: the hubs can be anywhere.  Two small kernels list the
-        // first kHeavyMaxWindowsNat heavy windows (tens of KB of stream-ordered
-        // scratch); teams of 16 waves take those, one wave each takes the rest.
+        // Natural order: the hubs can be anywhere.  Small kernels list the
+        // large windows (the ordered rule) for teams of 16 and the medium ones
+        // for teams of 4 (a 16-wave team holds a CU's LDS, 4 waves a quarter
+        // of it), in a few tens of KB of stream-ordered scratch; one wave each
+        // takes the rest, skipping the listed windows.
+        const HeavyClass large{kHeavyMinTiles, kHeavyMeanFactor, 0, 0, kHeavyMaxWindows};
+        const HeavyClass medium{kHeavyMinTilesNat, kHeavyMeanFactorNat, kHeavyMinTiles,
+                                kHeavyMeanFactor, kHeavyMaxWindowsNat};
         const int32_t nb = (int32_t)ceil_div(W, 256);
         const size_t words = (size_t)ceil_div(W, 32);
-        const size_t bytes = sizeof(int32_t) * ((size_t)kHeavyMaxWindowsNat + nb) +
+        const size_t bytes = sizeof(int32_t) * ((size_t)large.cap + medium.cap + 2 * (size_t)nb) +
                              sizeof(uint32_t) * words;
         void* scratch = nullptr;
         if (hipMallocAsync(&scratch, bytes, st) != hipSuccess) {
             (void)hipGetLastError();   // no stream-ordered pool: one launch as before
             return launch(p, H, scale, st);
         }
-        int32_t* list = reinterpret_cast<int32_t*>(scratch);
-        int32_t* counts = list + kHeavyMaxWindowsNat;
-        uint32_t* listed = reinterpret_cast<uint32_t*>(counts + nb);
+        int32_t* list_l = reinterpret_cast<int32_t*>(scratch);
+        int32_t* list_m = list_l + large.cap;
+        int32_t* counts_l = list_m + medium.cap;
+        int32_t* counts_m = counts_l + nb;
+        uint32_t* listed = reinterpret_cast<uint32_t*>(counts_m + nb);
         hipLaunchKernelGGL(heavy_count, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
-                           list, counts, listed);
+                           large, list_l, counts_l, listed, 1);
         hipLaunchKernelGGL(heavy_list, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
-                           counts, list, listed);
+                           large, counts_l, list_l, listed);
+        hipLaunchKernelGGL(heavy_count, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
+                           medium, list_m, counts_m, listed, 0);
+        hipLaunchKernelGGL(heavy_list, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
+                           medium, counts_m, list_m, listed);
         const hipError_t le = hipGetLastError();
         f3s_status s =
-            le == hipSuccess ? F3S_OK : hip_fail(le, "heavy window list", __FILE__, __LINE__);
-        if (s == F3S_OK) {
+            le == hipSuccess ? F3S_OK : hip_fail(le, "heavy window lists", __FILE__, __LINE__);
+        for (int c = 0; c < 2 && s == F3S_OK; ++c) {
+            const HeavyClass& hc = c == 0 ? large : medium;
             AttnParams ph = p;
-            ph.window_order = list;
+            ph.window_order = c == 0 ? list_l : list_m;
             ph.xcd_contiguous = 0;
-            ph.team = kTeamLarge;
-            ph.num_items = (int64_t)kHeavyMaxWindowsNat * kTeamLarge;
+            ph.team = c == 0 ? kTeamLarge : kTeamSmall;
+            ph.num_items = (int64_t)hc.cap * ph.team;
             ph.heavy_mode = 2;
-            ph.heavy_max = kHeavyMaxWindowsNat;
-            ph.heavy_min = kHeavyMinTilesNat;
-            ph.heavy_factor = kHeavyMeanFactorNat;
+            ph.heavy_max = hc.cap;
+            ph.heavy_min = hc.lo_min;
+            ph.heavy_factor = hc.lo_factor;
             s = launch(ph, H, scale, st);
         }
         if (s == F3S_OK) {

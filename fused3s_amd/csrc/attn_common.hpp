@@ -77,14 +77,15 @@ struct AttnParams {
     const uint32_t* heavy_listed;    // heavy_mode 3: bitmap of the windows a team launch took
 };
 
-// A window is heavy for the unplanned two-launch schedule when its tiles
-// exceed both a minimum and a multiple of the mean window: given a window
-// order, kHeavyMinTiles and kHeavyMeanFactor, and only the first
-// kHeavyMaxWindows order positions (the reference's descending order puts the
-// hubs there and runs the other windows big-first); in natural order, where
-// a window just under the threshold may start last, the lower
-// kHeavyMinTilesNat and kHeavyMeanFactorNat, and the first
-// kHeavyMaxWindowsNat heavy windows by index.
+// A window is heavy for the unplanned team launches when its tiles exceed
+// both a minimum and a multiple of the mean window: given a window order,
+// kHeavyMinTiles and kHeavyMeanFactor, and only the first kHeavyMaxWindows
+// order positions (the reference's descending order puts the hubs there and
+// runs the other windows big-first); in natural order, the first
+// kHeavyMaxWindows such windows by index (teams of 16) and the first
+// kHeavyMaxWindowsNat of those below it but above kHeavyMinTilesNat and
+// kHeavyMeanFactorNat (teams of 4), since a window just under the threshold
+// may start last.
 constexpr int32_t kHeavyMinTiles = 1024;
 constexpr int32_t kHeavyMeanFactor = 8;
 constexpr int32_t kHeavyMaxWindows = 512;

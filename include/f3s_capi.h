@@ -122,10 +122,12 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * share of the window's tiles, merged in LDS in a fixed order.  On larger
  * graphs, given d_window_order, the heavy windows among its first 512
  * entries (more than max(1024, 8 x mean) tiles) run as teams of 16 in a
- * launch of their own before the others; in natural order, the first 4,096
- * windows of more than max(512, 2 x mean) tiles do, listed by two small
- * kernels into scratch allocated and freed stream-ordered on `stream`
- * (hipMallocAsync / hipFreeAsync).  Every other path allocates nothing. */
+ * launch of their own before the others; in natural order, the first 512
+ * windows of more than max(1024, 8 x mean) tiles run as teams of 16 and the
+ * first 4,096 of more than max(512, 2 x mean) (but not more than the first
+ * bound) as teams of 4, listed by small kernels into scratch allocated and
+ * freed stream-ordered on `stream` (hipMallocAsync / hipFreeAsync).  Every
+ * other path allocates nothing. */
 f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                              float* O, const int32_t* d_window_offsets,
                              const int32_t* d_block_col, const uint16_t* d_tile_mask,

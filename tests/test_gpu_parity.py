@@ -561,8 +561,9 @@ def test_unplanned_heavy_windows(gpu):
 
 
 def test_unplanned_natural_order_heavy_cap(gpu):
-    # Natural order counts a window as heavy above max(512, 2 x mean) tiles
-    # and gives the first 4,096 of them by index to the team launch.  Here
+    # Natural order gives the first 4,096 windows by index of more than
+    # max(512, 2 x mean) tiles (and no more than max(1024, 8 x mean)) to a
+    # launch of 4-wave teams.  Here
     # 4,200 windows (every 4th of 16,800) hold exactly 600 tiles: the last
     # 104 run on one wave each, and the listing kernels' 256-window blocks
     # each hold 64 of them.  With a window order the rule is max(1024,
