@@ -150,6 +150,9 @@ def main() -> int:
     ap.add_argument("--heads", type=int, default=0,
                     help="override the configuration's head count (1 to 64); the line is "
                          "then not the configuration's own workload")
+    ap.add_argument("--unplanned", action="store_true",
+                    help="time the drop-in launch f3s_attention_fwd (each window whole, in "
+                         "the given order; the reference's launch) instead of a plan")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run device-to-device copies of this size (calibrates the "
@@ -213,27 +216,40 @@ def main() -> int:
     conv_ms = convert_phases_ms(csr, bsf, stream)
     use_sorted = args.order == "sorted" or (args.order == "auto" and c.kind != "sbm")
     order = f3s.window_order_device(bsf, stream) if use_sorted else None
-    ev0.record(stream)
-    plan = f3s.Plan(bsf, order, H=H, seg_tiles=args.seg, stream=stream)
-    if masked and not args.no_compile:
-        plan.compile(stream)
-    ev1.record(stream)
-    plan_ms = ev0.elapsed_ms(ev1)
+    plan = None
+    plan_ms = None
+    if not args.unplanned:
+        ev0.record(stream)
+        plan = f3s.Plan(bsf, order, H=H, seg_tiles=args.seg, stream=stream)
+        if masked and not args.no_compile:
+            plan.compile(stream)
+        ev1.record(stream)
+        plan_ms = ev0.elapsed_ms(ev1)
     occ_sum, mask_bits = f3s.bsf_stats(bsf, masked, stream)
     dQ, dK, dV = (f3s.DeviceArray.from_numpy(x.view(np.uint16), stream) for x in (Q, K, V))
     dO = f3s.DeviceArray((n, H, d), np.float32)
-    print(f"[bench] W={bsf.W} T={bsf.T} occ={occ_sum} items={plan.num_items} "
-          f"split={plan.num_split} seg={plan.seg_tiles} convert={conv_ms:.2f}ms "
-          f"plan={plan_ms:.2f}ms",
-          file=sys.stderr, flush=True)
+    if plan is not None:
+        print(f"[bench] W={bsf.W} T={bsf.T} occ={occ_sum} items={plan.num_items} "
+              f"split={plan.num_split} seg={plan.seg_tiles} convert={conv_ms:.2f}ms "
+              f"plan={plan_ms:.2f}ms",
+              file=sys.stderr, flush=True)
+
+        def one_pass():
+            plan.forward(dQ, dK, dV, dO, masked=masked, stream=stream)
+    else:
+        print(f"[bench] W={bsf.W} T={bsf.T} occ={occ_sum} unplanned convert={conv_ms:.2f}ms",
+              file=sys.stderr, flush=True)
+
+        def one_pass():
+            f3s.attention_fwd(dQ, dK, dV, dO, bsf, order, masked=masked, H=H, d=d, stream=stream)
 
     # cold first launch (the reference times exactly this, tests/test_fused_3s_v2.cu:126-137)
     ev0.record(stream)
-    plan.forward(dQ, dK, dV, dO, masked=masked, stream=stream)
+    one_pass()
     ev1.record(stream)
     cold_ms = ev0.elapsed_ms(ev1)
     for _ in range(args.warmup):
-        plan.forward(dQ, dK, dV, dO, masked=masked, stream=stream)
+        one_pass()
     stream.synchronize()
 
     # timed region: K steps bracketed by synchronisation; one event pair per
@@ -243,7 +259,7 @@ def main() -> int:
     t_start = time.perf_counter()
     for a, b in evs:
         a.record(stream)
-        plan.forward(dQ, dK, dV, dO, masked=masked, stream=stream)
+        one_pass()
         b.record(stream)
     stream.synchronize()
     f3s.synchronize()
@@ -262,7 +278,7 @@ def main() -> int:
     chunks = (occ_sum + 31) // 32 if masked else (bsf.T + 1) // 2
     flops_issued = chunks * H * 8 * (2 * 16 * 16 * 32)
     traffic = read_traffic(c.cfg, masked and not args.no_compile and args.order == "auto"
-                           and args.seg == 0 and not args.heads)
+                           and args.seg == 0 and not args.heads and not args.unplanned)
     res = {
         "metric": "fused attention edges/s + kernel us; achieved HBM GB/s (% of peak) on 1 MI355X",
         "value": nnz * args.steps / wall,
@@ -279,6 +295,7 @@ def main() -> int:
         "config": {"workload": f"cfg{c.cfg}: {c.name}" + (f" with H={H}" if args.heads else ""), "nodes": n, "edges": nnz, "heads": H,
                    "head_dim": d, "semantics": args.semantics,
                    "window_order": "descending workload" if use_sorted else "natural",
+                   "launch": "f3s_attention_fwd (unplanned)" if args.unplanned else "plan",
                    "row_windows": bsf.W,
                    "active_tiles": bsf.T, "attended_tile_columns": occ_sum},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -292,8 +309,8 @@ def main() -> int:
         "mfma_frac_issued": flops_issued / (kavg * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
         "converter_us": conv_ms * 1e3,
         "converter_end_to_end_us": conv_e2e_ms * 1e3,
-        "plan_us": plan_ms * 1e3,
-        "plan_compiled": bool(masked and not args.no_compile),
+        "plan_us": plan_ms * 1e3 if plan_ms is not None else None,
+        "plan_compiled": bool(masked and not args.no_compile and not args.unplanned),
         "device": f3s.device_name(),
     }
     if not args.no_cpu_baseline:
