@@ -270,8 +270,9 @@ def main() -> int:
 
     nbytes = alg_bytes(n, bsf.W, bsf.T, occ_sum, H, d, masked)
     achieved = nbytes / (kavg * 1e-3) / 1e9
-    # matrix-core work: the survey's tile model (4 products of 16x16x64 per
-    # active tile and head), and what the pass issues -- 8 MFMA 16x16x32 per
+    # matrix-core work: the reference's tile model (per active tile and head,
+    # S = Q K^T and O += P V, two products of 16x16x64 at 2 flops per
+    # multiply-add), and what the pass issues -- 8 MFMA 16x16x32 per
     # chunk of 32 gathered columns (masked: the attended columns, at least
     # occ_sum / 32 chunks; tile-dense: two tiles per chunk)
     flops_tile = bsf.T * 4 * 16 * 16 * d * H

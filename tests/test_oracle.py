@@ -9,8 +9,8 @@ How each oracle function is pinned (none is left "parity unpinned"):
                                     reference's stated sizes (meta.txt)
   orc_convert_count/fill            W=170 for Cora (README.md:140, the NCU
                                     grid of sc_csvs/v2_cora_ncu_results.csv);
-                                    the known answers restated in the build's
-                                    survey (T, sums, hashes); and invariants
+                                    known answers for the reference's input
+                                    (T, sums, hashes); and invariants
                                     that characterise the output completely:
                                     every edge's tile is listed with its bit
                                     set, no bit without an edge, ascending
