@@ -735,71 +735,110 @@ struct HeavyClass {
     int32_t cap;                 // list entries
 };
 
-__device__ __forceinline__ bool heavy_in_class(const int32_t* __restrict__ window_offsets,
-                                               int32_t W, int32_t w, const HeavyClass& hc)
+// Tiles of window w (-1 past the last window).
+__device__ __forceinline__ int32_t window_tiles(const int32_t* __restrict__ window_offsets,
+                                                int32_t W, int32_t w)
 {
-    if (w >= W) return false;
+    if (w >= W) return -1;
     const int32_t T = window_offsets[W];
     const int32_t tb = max(0, min(window_offsets[w], T));
     const int32_t te = max(tb, min(window_offsets[w + 1], T));
-    const int32_t t = te - tb;
+    return te - tb;
+}
+
+__device__ __forceinline__ bool heavy_in_class(int32_t t, int32_t T, int32_t W, const HeavyClass& hc)
+{
     return t > heavy_tiles(T, W, hc.lo_min, hc.lo_factor) &&
            (hc.hi_min <= 0 || t <= heavy_tiles(T, W, hc.hi_min, hc.hi_factor));
 }
 
-// heavy_count: per block, the number of its windows in the class; block 0
-// fills the list with -1; `zero_bits` also zeroes the block's bitmap words.
+// heavy_count: per block, the number of its windows in each of two disjoint
+// classes (counts[b] for a, counts[nb + b] for b); block 0 fills both lists
+// with -1, and each block zeroes its bitmap words.
 __global__ void __launch_bounds__(256)
-heavy_count(const int32_t* __restrict__ window_offsets, int32_t W, HeavyClass hc,
-            int32_t* __restrict__ list, int32_t* __restrict__ block_counts,
-            uint32_t* __restrict__ listed, int32_t zero_bits)
+heavy_count(const int32_t* __restrict__ window_offsets, int32_t W, HeavyClass a, HeavyClass b,
+            int32_t* __restrict__ list_a, int32_t* __restrict__ list_b,
+            int32_t* __restrict__ counts, uint32_t* __restrict__ listed)
 {
     const int32_t w = blockIdx.x * 256 + threadIdx.x;
-    if (blockIdx.x == 0)
-        for (int i = threadIdx.x; i < hc.cap; i += 256) list[i] = -1;
-    if (zero_bits && threadIdx.x < 8 &&
-        (int64_t)blockIdx.x * 8 + threadIdx.x < ((int64_t)W + 31) / 32)
+    if (blockIdx.x == 0) {
+        for (int i = threadIdx.x; i < a.cap; i += 256) list_a[i] = -1;
+        for (int i = threadIdx.x; i < b.cap; i += 256) list_b[i] = -1;
+    }
+    if (threadIdx.x < 8 && (int64_t)blockIdx.x * 8 + threadIdx.x < ((int64_t)W + 31) / 32)
         listed[blockIdx.x * 8 + threadIdx.x] = 0u;
-    const bool heavy = heavy_in_class(window_offsets, W, w, hc);
-    __shared__ int32_t wc[4];
-    const int32_t c = __popcll(__ballot(heavy));
-    if ((threadIdx.x & (kWave - 1)) == 0) wc[threadIdx.x / kWave] = c;
+    const int32_t T = W > 0 ? window_offsets[W] : 0;
+    const int32_t t = window_tiles(window_offsets, W, w);
+    const bool in_a = t >= 0 && heavy_in_class(t, T, W, a);
+    const bool in_b = t >= 0 && heavy_in_class(t, T, W, b);
+    __shared__ int32_t wc[2][4];
+    const int32_t ca = __popcll(__ballot(in_a));
+    const int32_t cb = __popcll(__ballot(in_b));
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        wc[0][threadIdx.x / kWave] = ca;
+        wc[1][threadIdx.x / kWave] = cb;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) block_counts[blockIdx.x] = wc[0] + wc[1] + wc[2] + wc[3];
+    if (threadIdx.x == 0) {
+        counts[blockIdx.x] = wc[0][0] + wc[0][1] + wc[0][2] + wc[0][3];
+        counts[gridDim.x + blockIdx.x] = wc[1][0] + wc[1][1] + wc[1][2] + wc[1][3];
+    }
 }
 
 // heavy_list: a window's rank in its class is the class's windows in earlier
-// blocks plus those before it in its block; ranks below the cap are listed
-// and their bits ORed into the bitmap (one lane per word).
+// blocks plus those before it in its block; ranks below the class's cap are
+// listed and their bits set in the bitmap (one lane per word).
 __global__ void __launch_bounds__(256)
-heavy_list(const int32_t* __restrict__ window_offsets, int32_t W, HeavyClass hc,
-           const int32_t* __restrict__ block_counts, int32_t* __restrict__ list,
-           uint32_t* __restrict__ listed)
+heavy_list(const int32_t* __restrict__ window_offsets, int32_t W, HeavyClass a, HeavyClass b,
+           const int32_t* __restrict__ counts, int32_t* __restrict__ list_a,
+           int32_t* __restrict__ list_b, uint32_t* __restrict__ listed)
 {
-    __shared__ int32_t red[4];
-    __shared__ int32_t wc[4];
+    __shared__ int32_t red[2][4];
+    __shared__ int32_t wc[2][4];
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    int32_t before = 0;
-    for (int32_t b = threadIdx.x; b < (int32_t)blockIdx.x; b += 256) before += block_counts[b];
-    before = wave_sum(before);
-    if (lane == 0) red[wid] = before;
+    int32_t before_a = 0, before_b = 0;
+    for (int32_t k = threadIdx.x; k < (int32_t)blockIdx.x; k += 256) {
+        before_a += counts[k];
+        before_b += counts[gridDim.x + k];
+    }
+    before_a = wave_sum(before_a);
+    before_b = wave_sum(before_b);
+    if (lane == 0) {
+        red[0][wid] = before_a;
+        red[1][wid] = before_b;
+    }
     __syncthreads();
-    before = red[0] + red[1] + red[2] + red[3];
-    if (before >= hc.cap) return;   // uniform
+    before_a = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    before_b = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    if (before_a >= a.cap && before_b >= b.cap) return;   // uniform
     const int32_t w = blockIdx.x * 256 + threadIdx.x;
-    const bool heavy = heavy_in_class(window_offsets, W, w, hc);
-    const uint64_t bal = __ballot(heavy);
-    if (lane == 0) wc[wid] = __popcll(bal);
+    const int32_t T = W > 0 ? window_offsets[W] : 0;
+    const int32_t t = window_tiles(window_offsets, W, w);
+    const bool in_a = t >= 0 && heavy_in_class(t, T, W, a);
+    const bool in_b = t >= 0 && heavy_in_class(t, T, W, b);
+    const uint64_t bal_a = __ballot(in_a);
+    const uint64_t bal_b = __ballot(in_b);
+    if (lane == 0) {
+        wc[0][wid] = __popcll(bal_a);
+        wc[1][wid] = __popcll(bal_b);
+    }
     __syncthreads();
-    int32_t rank = before + __popcll(bal & ((1ull << lane) - 1ull));
-    for (int v = 0; v < wid; ++v) rank += wc[v];
-    const bool take = heavy && rank < hc.cap;
-    if (take) list[rank] = w;
+    const uint64_t below = (1ull << lane) - 1ull;
+    int32_t rank_a = before_a + __popcll(bal_a & below);
+    int32_t rank_b = before_b + __popcll(bal_b & below);
+    for (int v = 0; v < wid; ++v) {
+        rank_a += wc[0][v];
+        rank_b += wc[1][v];
+    }
+    const bool take_a = in_a && rank_a < a.cap;
+    const bool take_b = in_b && rank_b < b.cap;
+    if (take_a) list_a[rank_a] = w;
+    if (take_b) list_b[rank_b] = w;
     // each wave owns its two bitmap words
-    const uint64_t tb = __ballot(take);
+    const uint64_t tb = __ballot(take_a || take_b);
     const int64_t word = ((int64_t)blockIdx.x * 256 + wid * kWave) / 32;
-    if (lane == 0 && word < ((int64_t)W + 31) / 32) listed[word] |= (uint32_t)tb;
-    if (lane == 1 && word + 1 < ((int64_t)W + 31) / 32) listed[word + 1] |= (uint32_t)(tb >> 32);
+    if (lane == 0 && word < ((int64_t)W + 31) / 32) listed[word] = (uint32_t)tb;
+    if (lane == 1 && word + 1 < ((int64_t)W + 31) / 32) listed[word + 1] = (uint32_t)(tb >> 32);
 }
 
 static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
@@ -862,7 +901,7 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
     p.xcd_contiguous = d_window_order == nullptr;
     hipStream_t st = as_stream(stream);
     if (p.team == 1 && !d_window_order && !wide_features(n, H) && W > kHeavyMaxWindows) {
-        // Natural order: the hubs can be anywhere.  Small kernels list the
+        // Natural order: the hubs can be anywhere.  Two small kernels list the
         // large windows (the ordered rule) for teams of 16 and the medium ones
         // for teams of 4 (a 16-wave team holds a CU's LDS, 4 waves a quarter
         // of it), in a few tens of KB of stream-ordered scratch; one wave each
@@ -881,17 +920,12 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
         }
         int32_t* list_l = reinterpret_cast<int32_t*>(scratch);
         int32_t* list_m = list_l + large.cap;
-        int32_t* counts_l = list_m + medium.cap;
-        int32_t* counts_m = counts_l + nb;
-        uint32_t* listed = reinterpret_cast<uint32_t*>(counts_m + nb);
+        int32_t* counts = list_m + medium.cap;   // 2 x nb
+        uint32_t* listed = reinterpret_cast<uint32_t*>(counts + 2 * nb);
         hipLaunchKernelGGL(heavy_count, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
-                           large, list_l, counts_l, listed, 1);
+                           large, medium, list_l, list_m, counts, listed);
         hipLaunchKernelGGL(heavy_list, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
-                           large, counts_l, list_l, listed);
-        hipLaunchKernelGGL(heavy_count, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
-                           medium, list_m, counts_m, listed, 0);
-        hipLaunchKernelGGL(heavy_list, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
-                           medium, counts_m, list_m, listed);
+                           large, medium, counts, list_l, list_m, listed);
         const hipError_t le = hipGetLastError();
         f3s_status s =
             le == hipSuccess ? F3S_OK : hip_fail(le, "heavy window lists", __FILE__, __LINE__);

@@ -125,7 +125,7 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * launch of their own before the others; in natural order, the first 512
  * windows of more than max(1024, 8 x mean) tiles run as teams of 16 and the
  * first 4,096 of more than max(512, 2 x mean) (but not more than the first
- * bound) as teams of 4, listed by small kernels into scratch allocated and
+ * bound) as teams of 4, listed by two small kernels into scratch allocated and
  * freed stream-ordered on `stream` (hipMallocAsync / hipFreeAsync).  Every
  * other path allocates nothing. */
 f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
