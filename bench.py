@@ -6,12 +6,18 @@ exponent 2.2, random node order, self-loops), d = 64, one head, Q/K/V
 workload order with heavy windows split by the plan.  A step is one fused
 pass over the whole graph with inputs already resident in HBM.
 
-Prints one JSON line: whole-job edges/s over K timed steps, the roofline
-of the fused kernel (algorithmic bytes / average launch time measured with
-HIP events on the launch stream), the reference's own CPU baseline
-(baselines/cpu_baseline.cpp, compiled under oracle/_ref, one thread as in
-the reference) and the CPU restatement of it on all available host cores
-(OpenMP, at most 16), both timed on this host.
+Prints one JSON line: whole-job edges/s over K timed steps and the roofline
+of the fused pass.  `roofline.achieved` is the pass's compulsory HBM bytes
+(Q read once, O written once, every K/V row the pass needs read once, its
+metadata read once) over the mean pass time from HIP events recorded on the
+launch stream, so `frac` cannot exceed 1 for a real measurement.  Beside it:
+the survey's gather model (every gathered K/V row counted), the traffic the
+L2 sends below itself as measured by rocprofv3 on this workload (HBM or the
+256 MB Infinity Cache: no gfx950 counter tells them apart), the matrix-core
+work, the reference's own semantics and launch shape timed on the same
+inputs after the timed region, the reference's CPU baseline
+(baselines/cpu_baseline.cpp compiled under oracle/_ref, one thread as in the
+reference) and the CPU restatement of it on all available host cores.
 """
 from __future__ import annotations
 
@@ -30,21 +36,66 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA
+ROW_BYTES = 128                # one fp16 row of one head at d = 64
+PARTIAL_BYTES = 4224           # (m, l, O) of one split-window segment and head
 
 
-def alg_bytes(n: int, W: int, T: int, occ_sum: int, H: int, d: int, masked: bool) -> int:
-    """Algorithmic HBM bytes of one pass: Q fp16 and O fp32 per row, window
-    offsets + order, per tile a column index (+ 32 B of row masks when
-    masked) and one K and one V fp16 row per attended (tile, column)."""
+def gather_model_bytes(n: int, W: int, T: int, occ_sum: int, H: int, d: int,
+                       masked: bool) -> int:
+    """The survey's byte model: Q fp16 and O fp32 per row, window offsets +
+    order, per tile a column index (+ 32 B of row masks when masked) and one
+    K and one V fp16 row per attended (tile, column).  Counts every gather,
+    including those the caches serve."""
     return (n * H * d * (2 + 4) + (W + 1) * 4 + W * 4 + T * (4 + (32 if masked else 0))
             + occ_sum * H * d * 2 * 2)
+
+
+def kv_rows_needed(n: int, ci: np.ndarray, block_col: np.ndarray | None, masked: bool) -> int:
+    """Distinct K/V rows the pass reads: the columns with at least one edge
+    (masked), or every node < n of every active block column (tile-dense)."""
+    if masked:
+        return int(np.count_nonzero(np.bincount(ci, minlength=n)))
+    W = (n + 15) // 16
+    act = np.flatnonzero(np.bincount(block_col, minlength=W))
+    return int(np.minimum(16, n - 16 * act).sum())
+
+
+def compulsory_bytes(n: int, H: int, W: int, T: int, kv_rows: int, masked: bool,
+                     launch: str, ps: dict | None) -> int:
+    """HBM bytes one pass cannot avoid: Q once (fp16), O once (fp32), each
+    needed K and V row once, and the metadata the launch reads once --
+    compiled chunk records (256 B), items (16 B) and chunk bases, or the
+    tile lists (4 B per tile, + 32 B of masks when masked) with the window
+    offsets and order -- plus split-window partials written and read back."""
+    b = n * H * ROW_BYTES * 3 + kv_rows * H * ROW_BYTES * 2
+    if launch == "plan":
+        items = ps["masked_items"] if masked else ps["dense_items"]
+        slots = ps["masked_slots"] if masked else ps["dense_slots"]
+        b += items * 16 + slots * H * PARTIAL_BYTES * 2
+        if masked and ps["num_chunks"]:
+            b += ps["num_chunks"] * 256 + (items + 1) * 4
+        else:
+            b += T * (4 + (32 if masked else 0))
+    else:
+        b += T * (4 + (32 if masked else 0)) + (W + 1) * 4 + W * 4
+    return int(b)
+
+
+def read_profile(path: Path, key: str) -> float | None:
+    """`key value` line of a committed rocprofv3 summary."""
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 2 and parts[0] == key:
+            return float(parts[1])
+    return None
 
 
 def convert_phases_ms(csr, bsf, stream) -> float:
     """GPU time of f3s_convert_csr_to_bsf's count call plus its fill call into
     the outputs of an earlier conversion of the same CSR (HIP events on the
-    launch stream around each call; the caller's allocation between the two
-    calls is left out)."""
+    launch stream around each call)."""
     import fused3s_amd as f3s
     from fused3s_amd import _lib
     from fused3s_amd.device import check
@@ -66,20 +117,17 @@ def convert_phases_ms(csr, bsf, stream) -> float:
     return e[0].elapsed_ms(e[1]) + e[2].elapsed_ms(e[3])
 
 
-def read_traffic(cfg: int, default_pass: bool) -> float | None:
-    """HBM bytes per launch of the fused pass from the committed rocprofv3
-    --pmc summary of this configuration (profiles/pmc_traffic_cfg<N>.txt:
-    'bytes_per_launch <value>'); those were measured on the default pass
-    (masked, compiled plan, default order and segments), so other passes get
-    None."""
-    p = ROOT / "profiles" / f"pmc_traffic_cfg{cfg}.txt"
-    if not default_pass or not p.exists():
-        return None
-    for line in p.read_text().splitlines():
-        parts = line.split()
-        if len(parts) == 2 and parts[0] == "bytes_per_launch":
-            return float(parts[1])
-    return None
+def time_passes(f3s, one_pass, stream, reps: int) -> np.ndarray:
+    """Per-pass milliseconds from HIP events on the launch stream, after one
+    untimed pass."""
+    one_pass()
+    evs = [(f3s.Event(), f3s.Event()) for _ in range(reps)]
+    for a, b in evs:
+        a.record(stream)
+        one_pass()
+        b.record(stream)
+    stream.synchronize()
+    return np.array([a.elapsed_ms(b) for a, b in evs])
 
 
 def cpu_baseline(rp, ci, Q, K, V, n: int, d: int) -> dict | None:
@@ -153,6 +201,9 @@ def main() -> int:
     ap.add_argument("--unplanned", action="store_true",
                     help="time the drop-in launch f3s_attention_fwd (each window whole, in "
                          "the given order; the reference's launch) instead of a plan")
+    ap.add_argument("--no-reference-launches", action="store_true",
+                    help="skip timing the reference's semantics and launch shape after the "
+                         "timed region")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run device-to-device copies of this size (calibrates the "
@@ -205,29 +256,51 @@ def main() -> int:
     csr = f3s.DeviceCSR(rp, ci, stream)
     ev0, ev1 = f3s.Event(), f3s.Event()
     # converter (timed separately; not part of a step): end to end through
-    # the Python wrapper (output allocation included), and the two C-ABI
-    # phases alone into the already allocated outputs
-    bsf = f3s.convert_device(csr, masks=True, stream=stream)
-    f3s.synchronize()
-    t_conv = time.perf_counter()
-    bsf = f3s.convert_device(csr, masks=True, stream=stream)
-    f3s.synchronize()
-    conv_e2e_ms = (time.perf_counter() - t_conv) * 1e3
+    # the Python wrapper (output allocation included; host wall time to
+    # completion), the first call of the process and the median of four
+    # later ones (the allocator then reuses the freed outputs), and the two
+    # C-ABI phases alone into already allocated outputs
+    conv_e2e = []
+    bsf = None
+    for _ in range(5):
+        bsf = None
+        f3s.synchronize()
+        t_conv = time.perf_counter()
+        bsf = f3s.convert_device(csr, masks=True, stream=stream)
+        f3s.synchronize()
+        conv_e2e.append((time.perf_counter() - t_conv) * 1e3)
+    conv_e2e_first_ms, conv_e2e_ms = conv_e2e[0], float(np.median(conv_e2e[1:]))
     conv_ms = convert_phases_ms(csr, bsf, stream)
     use_sorted = args.order == "sorted" or (args.order == "auto" and c.kind != "sbm")
     order = f3s.window_order_device(bsf, stream) if use_sorted else None
     plan = None
     plan_ms = None
-    if not args.unplanned:
-        ev0.record(stream)
-        plan = f3s.Plan(bsf, order, H=H, seg_tiles=args.seg, stream=stream)
+    compiled = masked and not args.no_compile and not args.unplanned
+
+    def make_plan():
+        p = f3s.Plan(bsf, order, H=H, seg_tiles=args.seg, stream=stream)
         if masked and not args.no_compile:
-            plan.compile(stream)
-        ev1.record(stream)
-        plan_ms = ev0.elapsed_ms(ev1)
+            p.compile(stream)
+        return p
+
+    plan_first_ms = None
+    if not args.unplanned:
+        # plan creation (+ compile) through the Python wrapper, host wall
+        # time to completion: the first of the process and the median of
+        # four later ones, as for the converter
+        times = []
+        for _ in range(5):
+            plan = None
+            f3s.synchronize()
+            t_plan = time.perf_counter()
+            plan = make_plan()
+            f3s.synchronize()
+            times.append((time.perf_counter() - t_plan) * 1e3)
+        plan_first_ms, plan_ms = times[0], float(np.median(times[1:]))
     occ_sum, mask_bits = f3s.bsf_stats(bsf, masked, stream)
     dQ, dK, dV = (f3s.DeviceArray.from_numpy(x.view(np.uint16), stream) for x in (Q, K, V))
     dO = f3s.DeviceArray((n, H, d), np.float32)
+    ps = plan.stats() if plan is not None else None
     if plan is not None:
         print(f"[bench] W={bsf.W} T={bsf.T} occ={occ_sum} items={plan.num_items} "
               f"split={plan.num_split} seg={plan.seg_tiles} convert={conv_ms:.2f}ms "
@@ -253,7 +326,7 @@ def main() -> int:
     stream.synchronize()
 
     # timed region: K steps bracketed by synchronisation; one event pair per
-    # launch on the launch stream gives the kernel's own duration
+    # launch on the launch stream gives the pass's own duration
     evs = [(f3s.Event(), f3s.Event()) for _ in range(args.steps)]
     f3s.synchronize()
     t_start = time.perf_counter()
@@ -268,18 +341,27 @@ def main() -> int:
     ms_per_step = wall * 1e3 / args.steps
     kavg = float(kern_ms.mean())
 
-    nbytes = alg_bytes(n, bsf.W, bsf.T, occ_sum, H, d, masked)
-    achieved = nbytes / (kavg * 1e-3) / 1e9
-    # matrix-core work: the reference's tile model (per active tile and head,
-    # S = Q K^T and O += P V, two products of 16x16x64 at 2 flops per
-    # multiply-add), and what the pass issues -- 8 MFMA 16x16x32 per
-    # chunk of 32 gathered columns (masked: the attended columns, at least
-    # occ_sum / 32 chunks; tile-dense: two tiles per chunk)
+    launch = "unplanned" if args.unplanned else "plan"
+    kv_rows = {True: kv_rows_needed(n, ci, None, True)}
+    hb_bcol = None
+    if not masked or not args.no_reference_launches:
+        hb_bcol = bsf.block_col.numpy()
+        kv_rows[False] = kv_rows_needed(n, ci, hb_bcol, False)
+    need = compulsory_bytes(n, H, bsf.W, bsf.T, kv_rows[masked], masked, launch, ps)
+    achieved = need / (kavg * 1e-3) / 1e9
+    gbytes = gather_model_bytes(n, bsf.W, bsf.T, occ_sum, H, d, masked)
+    # matrix-core work: what the pass issues -- 8 MFMA 16x16x32 per chunk of
+    # 32 gathered columns (masked: the attended columns, at least occ_sum / 32
+    # chunks; tile-dense: two tiles per chunk) -- and the reference's tile
+    # model (per active tile and head, S = Q K^T and O += P V, two products of
+    # 16x16x64 at 2 flops per multiply-add), a work figure, not a rate
     flops_tile = bsf.T * 4 * 16 * 16 * d * H
     chunks = (occ_sum + 31) // 32 if masked else (bsf.T + 1) // 2
     flops_issued = chunks * H * 8 * (2 * 16 * 16 * 32)
-    traffic = read_traffic(c.cfg, masked and not args.no_compile and args.order == "auto"
-                           and args.seg == 0 and not args.heads and not args.unplanned)
+    default_pass = (compiled and args.order == "auto" and args.seg == 0 and not args.heads)
+    prof = ROOT / "profiles" / f"pmc_traffic_cfg{c.cfg}.txt"
+    below = read_profile(prof, "bytes_per_launch") if default_pass else None
+    below_us = read_profile(prof, "kernel_avg_us") if default_pass else None
     res = {
         "metric": "fused attention edges/s + kernel us; achieved HBM GB/s (% of peak) on 1 MI355X",
         "value": nnz * args.steps / wall,
@@ -300,20 +382,77 @@ def main() -> int:
                    "row_windows": bsf.W,
                    "active_tiles": bsf.T, "attended_tile_columns": occ_sum},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": below,
+                     "bytes_per_launch": need,
+                     "bytes_model": "compulsory: Q fp16 + O fp32 once per row, each needed K and "
+                                    "V row once, launch metadata once (compiled chunk records "
+                                    "256 B, items 16 B), split-window partials written and "
+                                    "read back",
+                     "traffic_kind": "rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 per launch "
+                                     "(copy-calibrated): traffic below the L2, HBM or the 256 MB "
+                                     "Infinity Cache (no gfx950 counter separates them); read "
+                                     "from the committed profile of this workload",
+                     "traffic_source": str(prof.relative_to(ROOT)) if below else None},
+        "gather_model": {"bytes_per_launch": gbytes, "GBps": gbytes / (kavg * 1e-3) / 1e9,
+                         "note": "every gathered K/V row counted once per attending tile "
+                                 "(the survey's model); L2 and the Infinity Cache serve part "
+                                 "of it, so this rate can exceed the HBM peak"},
+        "below_l2": ({"bytes_per_launch": below, "GBps": below / (kavg * 1e-3) / 1e9,
+                      "frac_of_hbm_peak": below / (kavg * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                      "profiled_kernel_avg_us": below_us, "kind": "HBM + Infinity Cache",
+                      "source": str(prof.relative_to(ROOT))} if below else None),
+        "mfma": {"issued_tflop_per_pass": flops_issued / 1e12,
+                 "issued_frac_of_peak": flops_issued / (kavg * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
+                 "tile_model_tflop_per_pass": flops_tile / 1e12},
         "cpu_baseline": None,
         "cpu_baseline_all_cores": None,
         "kernel_us": {"mean": kavg * 1e3, "min": float(kern_ms.min()) * 1e3,
                       "median": float(np.median(kern_ms)) * 1e3, "cold_first_launch": cold_ms * 1e3},
-        "alg_bytes_per_launch": nbytes,
-        "mfma_frac_tile_model": flops_tile / (kavg * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
-        "mfma_frac_issued": flops_issued / (kavg * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
         "converter_us": conv_ms * 1e3,
         "converter_end_to_end_us": conv_e2e_ms * 1e3,
+        "converter_end_to_end_first_us": conv_e2e_first_ms * 1e3,
         "plan_us": plan_ms * 1e3 if plan_ms is not None else None,
-        "plan_compiled": bool(masked and not args.no_compile and not args.unplanned),
+        "plan_first_us": plan_first_ms * 1e3 if plan_first_ms is not None else None,
+        "plan_compiled": compiled,
         "device": f3s.device_name(),
     }
+
+    if not args.no_reference_launches:
+        # The reference's own semantics (tile-dense, src/fused3s_v2.cu:145-228)
+        # and launch shape (every window whole, descending order, one launch:
+        # tests/test_fused_3s_v2.cu:124-137) on the same inputs, after the
+        # timed region; per-pass times from events on the launch stream.
+        print("[bench] timing the reference's semantics and launch shapes ...", file=sys.stderr,
+              flush=True)
+        sorted_order = order if use_sorted else f3s.window_order_device(bsf, stream)
+        ref_plan = plan if plan is not None else make_plan()
+        rps = ref_plan.stats()
+        legs = {}
+        reps_m = max(3, min(20, args.steps))
+        reps_d = max(3, min(5, args.steps))
+
+        def leg(name, fn, sem_masked, lnch, reps):
+            t = time_passes(f3s, fn, stream, reps)
+            mean = float(t.mean())
+            b = compulsory_bytes(n, H, bsf.W, bsf.T, kv_rows[sem_masked], sem_masked, lnch, rps)
+            legs[name] = {"kernel_us": mean * 1e3, "edges_per_s": nnz / (mean * 1e-3),
+                          "passes": reps, "compulsory_bytes": b,
+                          "roofline_frac": b / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+        leg("tile_dense_planned",
+            lambda: ref_plan.forward(dQ, dK, dV, dO, masked=False, stream=stream),
+            False, "plan", reps_d)
+        for nm, sem in (("masked", True), ("tile_dense", False)):
+            leg(f"dropin_descending_{nm}",
+                lambda sem=sem: f3s.attention_fwd(dQ, dK, dV, dO, bsf, sorted_order, masked=sem,
+                                                  H=H, d=d, stream=stream),
+                sem, "unplanned", reps_m if sem else reps_d)
+        leg("dropin_natural_masked",
+            lambda: f3s.attention_fwd(dQ, dK, dV, dO, bsf, None, masked=True, H=H, d=d,
+                                      stream=stream),
+            True, "unplanned", reps_m)
+        res["reference_launches"] = legs
+
     if not args.no_cpu_baseline:
         print("[bench] timing the reference CPU baseline ...", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(rp, ci, Q.astype(np.float32), K.astype(np.float32),

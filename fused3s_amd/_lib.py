@@ -30,6 +30,7 @@ HIP_API = {
     "f3s_device_name": (c_i32, [C.c_char_p, c_i32]),
     "f3s_malloc": (c_i32, [P_vp, c_u64]),
     "f3s_free": (c_i32, [c_vp]),
+    "f3s_release_cached_memory": (c_i32, []),
     "f3s_memcpy_h2d": (c_i32, [c_vp, c_vp, c_u64, c_vp]),
     "f3s_memcpy_d2h": (c_i32, [c_vp, c_vp, c_u64, c_vp]),
     "f3s_memcpy_d2d": (c_i32, [c_vp, c_vp, c_u64, c_vp]),
@@ -56,6 +57,7 @@ HIP_API = {
     "f3s_plan_destroy": (c_i32, [c_vp]),
     "f3s_plan_compile": (c_i32, [c_vp, c_vp, c_vp, c_i32, c_vp]),
     "f3s_plan_info": (c_i32, [c_vp, P_i64, P_i64, P_i64, P_i32]),
+    "f3s_plan_stats": (c_i32, [c_vp, P_i64, P_i64, P_i64, P_i64, P_i64]),
     "f3s_attention_fwd_planned": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                           c_i32, c_i32, c_i32, c_f32, c_vp]),
 }

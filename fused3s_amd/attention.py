@@ -75,6 +75,14 @@ class Plan:
                                           bsf.n, stream.handle if stream else None),
               "f3s_plan_compile")
 
+    def stats(self) -> dict:
+        """f3s_plan_stats: compiled chunks and, per item set, items and
+        split-window partial slots."""
+        v = [C.c_int64() for _ in range(5)]
+        check(_lib.hip().f3s_plan_stats(self.handle, *(C.byref(x) for x in v)), "f3s_plan_stats")
+        return dict(zip(("num_chunks", "masked_items", "masked_slots", "dense_items",
+                         "dense_slots"), (int(x.value) for x in v)))
+
     def forward(self, Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray,
                 masked: bool = True, d: int = 64, scale: float = 1.0,
                 stream: Stream | None = None) -> None:

@@ -472,29 +472,73 @@ hipError_t warm_attention(hipStream_t s)
 
 // ----------------------------------------------------------------- planner
 
+// Segment sizes of an automatic plan.  A window is cut into segments only
+// when it is well above the mean window (4x masked, 2x tile-dense: cutting
+// every window of a uniform graph just adds merge traffic) and a large share
+// of one wave slot's part of the pass (5,120 slots; a tenth of it for
+// tile-dense).  seg[0] serves masked passes, seg[1] tile-dense ones.
+__host__ __device__ __forceinline__ void auto_segments(int64_t T, int32_t W, int32_t H,
+                                                       int64_t seg[2])
+{
+    const int64_t mean = W > 0 ? (T + W - 1) / W : 0;
+    int64_t m = 256, dd = 16;
+    if (4 * mean > m) m = 4 * mean;
+    if ((T * H + 8191) / 8192 > m) m = (T * H + 8191) / 8192;
+    if (2 * mean > dd) dd = 2 * mean;
+    if ((T * H + 51199) / 51200 > dd) dd = (T * H + 51199) / 51200;
+    seg[0] = m < INT32_MAX ? m : INT32_MAX;
+    seg[1] = dd < INT32_MAX ? dd : INT32_MAX;
+}
+
+// Work items per order position for one or two item sets: counts[3 k + 0]
+// items, [3 k + 1] partial slots, [3 k + 2] split windows of set k, each
+// [W].  seg_fixed > 0 is the one set's segment size; 0 takes the automatic
+// sizes from T = offs[W] (thread 0 also reports T and the sizes in info).
 __global__ void plan_count(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
-                           int32_t W, int32_t seg, int32_t team, int32_t* __restrict__ nitems,
-                           int32_t* __restrict__ nslots, int32_t* __restrict__ nsplit)
+                           int32_t W, int32_t H, int32_t seg_fixed, int32_t nsets, int32_t team0,
+                           int32_t team1, int32_t* __restrict__ counts, int64_t* __restrict__ info)
 {
     const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
+    const int32_t T = W > 0 ? max(0, offs[W]) : 0;
+    int64_t seg[2];
+    if (seg_fixed > 0) {
+        seg[0] = seg[1] = seg_fixed;
+    } else {
+        auto_segments(T, W, H, seg);
+    }
+    if (L == 0) {
+        info[0] = T;
+        info[1] = seg[0];
+        info[2] = seg[1];
+    }
     if (L >= W) return;
     const int32_t w = order ? order[L] : L;
-    if (team > 1) {   // a team's items, merged in LDS: no partials
-        nitems[L] = team;
-        nslots[L] = 0;
-        nsplit[L] = 0;
-        return;
-    }
-    int32_t ns = 1;
+    int32_t nt = 0;
     if (w >= 0 && w < W) {
-        const int32_t T = offs[W];
         const int32_t tb = max(0, min(offs[w], T)), te = max(tb, min(offs[w + 1], T));
-        const int32_t nt = te - tb;
-        if (nt > seg) ns = (nt + seg - 1) / seg;
+        nt = te - tb;
     }
-    nitems[L] = ns;
-    nslots[L] = ns > 1 ? ns : 0;
-    nsplit[L] = ns > 1 ? 1 : 0;
+    for (int k = 0; k < nsets; ++k) {
+        const int32_t team = k == 0 ? team0 : team1;
+        int32_t ns = 1;
+        if (team > 1) {
+            ns = team;   // a team's items, merged in LDS: no partials
+        } else if (nt > seg[k]) {
+            ns = (int32_t)((nt + seg[k] - 1) / seg[k]);
+        }
+        const bool split = team == 1 && ns > 1;
+        counts[(3 * k + 0) * (int64_t)W + L] = ns;
+        counts[(3 * k + 1) * (int64_t)W + L] = split ? ns : 0;
+        counts[(3 * k + 2) * (int64_t)W + L] = split ? 1 : 0;
+    }
+}
+
+// info[3 + j] = total of scanned count array j (bases[j][W]).
+__global__ void plan_totals(const int64_t* __restrict__ bases, int32_t W, int32_t arrays,
+                            int64_t* __restrict__ info)
+{
+    const int j = threadIdx.x;
+    if (j < arrays) info[3 + j] = bases[(int64_t)j * ((int64_t)W + 1) + W];
 }
 
 __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
@@ -610,57 +654,73 @@ plan_columns(const Item* __restrict__ items, int64_t num_items,
 
 namespace f3s {
 
-static f3s_status build_items(f3s_item_set& set, const int32_t* d_window_offsets,
-                              const int32_t* d_window_order, int32_t W, int32_t H, int64_t seg,
-                              int32_t team, hipStream_t st)
+// Lays out a plan's work items: counts for every item set in one pass, one
+// host round trip for their totals (and, for automatic plans, T and the
+// segment sizes computed on the device), then the item lists; the partial
+// buffer is shared by the sets (a plan serves one pass at a time).
+static f3s_status build_plan_sets(f3s_plan* p, const int32_t* d_window_offsets,
+                                  const int32_t* d_window_order, int32_t seg_tiles,
+                                  hipStream_t st)
 {
-    if (seg > INT32_MAX) seg = INT32_MAX;
-    set.seg = (int32_t)seg;
-    set.team = team;
-    DeviceBuffer cnt_items, cnt_slots, cnt_split, base_items, base_slots, base_split, tmp;
-    f3s_status s;
-    if ((s = cnt_items.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
-        (s = cnt_slots.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
-        (s = cnt_split.reserve(sizeof(int32_t) * (size_t)W)) != F3S_OK ||
-        (s = base_items.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
-        (s = base_slots.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
-        (s = base_split.reserve(sizeof(int64_t) * ((size_t)W + 1))) != F3S_OK ||
-        (s = tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(W))) != F3S_OK)
-        return s;
-    auto* ci = reinterpret_cast<int32_t*>(cnt_items.ptr);
-    auto* cs = reinterpret_cast<int32_t*>(cnt_slots.ptr);
-    auto* cp = reinterpret_cast<int32_t*>(cnt_split.ptr);
-    auto* bi = reinterpret_cast<int64_t*>(base_items.ptr);
-    auto* bs = reinterpret_cast<int64_t*>(base_slots.ptr);
-    auto* bp = reinterpret_cast<int64_t*>(base_split.ptr);
-    if (W > 0) {
-        hipLaunchKernelGGL(plan_count, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
-                           d_window_offsets, d_window_order, W, set.seg, team, ci, cs, cp);
-        F3S_HIP(hipGetLastError());
-    }
-    auto* tp = reinterpret_cast<int64_t*>(tmp.ptr);
-    F3S_TRY(exclusive_scan_i32_to_i64(ci, bi, W, tp, st));
-    F3S_TRY(exclusive_scan_i32_to_i64(cs, bs, W, tp, st));
-    F3S_TRY(exclusive_scan_i32_to_i64(cp, bp, W, tp, st));
-    int64_t totals[3] = {0, 0, 0};
-    F3S_HIP(hipMemcpyAsync(&totals[0], bi + W, 8, hipMemcpyDeviceToHost, st));
-    F3S_HIP(hipMemcpyAsync(&totals[1], bs + W, 8, hipMemcpyDeviceToHost, st));
-    F3S_HIP(hipMemcpyAsync(&totals[2], bp + W, 8, hipMemcpyDeviceToHost, st));
+    const int32_t W = p->W, H = p->H;
+    const bool automatic = seg_tiles == 0;
+    const int32_t team_m = automatic ? team_for(W, H, true) : 1;
+    const int32_t team_d = automatic ? team_for(W, H, false) : 1;
+    const int32_t nsets = automatic ? 2 : 1;
+    const int arrays = 3 * nsets;
+    const size_t cnt_bytes = sizeof(int32_t) * (size_t)arrays * (size_t)W;
+    const size_t base_bytes = sizeof(int64_t) * (size_t)arrays * ((size_t)W + 1);
+    const size_t tmp_bytes = sizeof(int64_t) * (size_t)scan_tmp_elems(W);
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    StreamBuffer buf(st);
+    F3S_TRY(buf.reserve(256 + al(cnt_bytes) + al(base_bytes) + al(tmp_bytes)));
+    char* q = static_cast<char*>(buf.ptr);
+    int64_t* info = reinterpret_cast<int64_t*>(q);           // [0] T, [1..2] segs, [3..] totals
+    int32_t* counts = reinterpret_cast<int32_t*>(q + 256);
+    int64_t* bases = reinterpret_cast<int64_t*>(q + 256 + al(cnt_bytes));
+    int64_t* tmp = reinterpret_cast<int64_t*>(q + 256 + al(cnt_bytes) + al(base_bytes));
+    hipLaunchKernelGGL(plan_count, dim3((unsigned)ceil_div(W > 0 ? W : 1, 256)), dim3(256), 0, st,
+                       d_window_offsets, d_window_order, W, H, seg_tiles, nsets, team_m, team_d,
+                       counts, info);
+    F3S_HIP(hipGetLastError());
+    for (int j = 0; j < arrays; ++j)
+        F3S_TRY(exclusive_scan_i32_to_i64(counts + (size_t)j * W, bases + (size_t)j * (W + 1), W,
+                                          tmp, st));
+    hipLaunchKernelGGL(plan_totals, dim3(1), dim3(64), 0, st, bases, W, arrays, info);
+    F3S_HIP(hipGetLastError());
+    int64_t* h = host_staging();
+    F3S_HIP(hipMemcpyAsync(h, info, sizeof(int64_t) * (3 + arrays), hipMemcpyDeviceToHost, st));
     F3S_HIP(hipStreamSynchronize(st));
-    set.num_items = totals[0];
-    set.num_slots = totals[1];
-    set.num_split = totals[2];
-    F3S_TRY(set.items.reserve(sizeof(Item) * (size_t)(set.num_items + 1)));
-    F3S_TRY(set.splits.reserve(sizeof(SplitInfo) * (size_t)(set.num_split + 1)));
-    F3S_TRY(set.partials.reserve(sizeof(float) * (size_t)kPartialFloats * H *
-                                 (size_t)(set.num_slots + 1)));
-    if (W > 0) {
+    p->T = h[0];
+    const int32_t seg_m = (int32_t)h[1], seg_d = (int32_t)h[2];
+    p->has_dense = automatic && (team_d != team_m || (team_d == 1 && seg_d != seg_m));
+    int64_t max_slots = 0;
+    for (int k = 0; k < nsets; ++k) {
+        f3s_item_set& set = k == 0 ? p->masked : p->dense;
+        if (k == 1 && !p->has_dense) break;
+        set.seg = k == 0 ? seg_m : seg_d;
+        set.team = k == 0 ? team_m : team_d;
+        set.num_items = h[3 + 3 * k];
+        set.num_slots = h[3 + 3 * k + 1];
+        set.num_split = h[3 + 3 * k + 2];
+        if (set.num_slots > max_slots) max_slots = set.num_slots;
+        F3S_TRY(set.items.reserve(sizeof(Item) * (size_t)(set.num_items + 1), st));
+        F3S_TRY(set.splits.reserve(sizeof(SplitInfo) * (size_t)(set.num_split + 1), st));
+    }
+    F3S_TRY(p->partials.reserve(sizeof(float) * (size_t)kPartialFloats * H * (size_t)(max_slots + 1),
+                                st));
+    for (int k = 0; k < nsets && W > 0; ++k) {
+        if (k == 1 && !p->has_dense) break;
+        f3s_item_set& set = k == 0 ? p->masked : p->dense;
+        const int64_t* bk = bases + (size_t)3 * k * (W + 1);
         hipLaunchKernelGGL(plan_fill, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
-                           d_window_offsets, d_window_order, W, set.seg, team, bi, bs, bp,
+                           d_window_offsets, d_window_order, W, set.seg, set.team, bk,
+                           bk + (W + 1), bk + 2 * (size_t)(W + 1),
                            reinterpret_cast<Item*>(set.items.ptr),
                            reinterpret_cast<SplitInfo*>(set.splits.ptr));
         F3S_HIP(hipGetLastError());
     }
+    // the plan is complete (and its memory usable on any stream) on return
     F3S_HIP(hipStreamSynchronize(st));
     return F3S_OK;
 }
@@ -913,12 +973,9 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
         const size_t words = (size_t)ceil_div(W, 32);
         const size_t bytes = sizeof(int32_t) * ((size_t)large.cap + medium.cap + 2 * (size_t)nb) +
                              sizeof(uint32_t) * words;
-        void* scratch = nullptr;
-        if (hipMallocAsync(&scratch, bytes, st) != hipSuccess) {
-            (void)hipGetLastError();   // no stream-ordered pool: one launch as before
-            return launch(p, H, scale, st);
-        }
-        int32_t* list_l = reinterpret_cast<int32_t*>(scratch);
+        StreamBuffer scratch(st);   // returned to the pool in stream order, after the launches
+        F3S_TRY(scratch.reserve(bytes));
+        int32_t* list_l = reinterpret_cast<int32_t*>(scratch.ptr);
         int32_t* list_m = list_l + large.cap;
         int32_t* counts = list_m + medium.cap;   // 2 x nb
         uint32_t* listed = reinterpret_cast<uint32_t*>(counts + 2 * nb);
@@ -947,10 +1004,7 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
             p.heavy_listed = listed;
             s = launch(p, H, scale, st);
         }
-        const hipError_t fe = hipFreeAsync(scratch, st);   // after the launches, in stream order
-        if (s != F3S_OK) return s;
-        F3S_HIP(fe);
-        return F3S_OK;
+        return s;
     }
     if (p.team == 1 && d_window_order && !wide_features(n, H)) {
         // Without a plan a hub window would run on one wave.  Given a window
@@ -991,11 +1045,6 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     clear_error();
     hipStream_t st = as_stream(stream);
 
-    int32_t T32 = 0;
-    if (W > 0) {
-        F3S_HIP(hipMemcpyAsync(&T32, d_window_offsets + W, sizeof T32, hipMemcpyDeviceToHost, st));
-        F3S_HIP(hipStreamSynchronize(st));
-    }
     f3s_plan* p = new (std::nothrow) f3s_plan();
     if (!p) {
         set_error("f3s_plan_create: out of host memory");
@@ -1004,27 +1053,11 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     p->W = W;
     p->H = H;
     p->natural_order = d_window_order == nullptr;
-    p->T = T32;
-    // Automatic plans.  A window is cut into segments only when it is well
-    // above the mean window (4x masked, 2x tile-dense: cutting every window
-    // of a uniform graph just adds merge traffic) and a large share of one
-    // wave slot's part of the pass (5,120 slots; a tenth of it for
-    // tile-dense).  Graphs whose windows leave most SIMDs idle run teams
+    // Automatic plans give tile-dense passes their own, finer item set (a
+    // tile-dense chunk costs two whole tiles, ~15x a masked chunk per tile
+    // on sparse graphs); graphs whose windows leave most SIMDs idle run teams
     // instead (team_for), as the unplanned launch does.
-    int64_t seg_m = seg_tiles, seg_d = 0;
-    int32_t team_m = 1, team_d = 1;
-    if (seg_tiles == 0) {
-        const int64_t mean = W > 0 ? ceil_div(p->T, W) : 0;
-        team_m = team_for(W, H, true);
-        team_d = team_for(W, H, false);
-        seg_m = std::max<int64_t>({256, 4 * mean, ceil_div(p->T * H, 8192)});
-        seg_d = std::max<int64_t>({16, 2 * mean, ceil_div(p->T * H, 51200)});
-        p->has_dense = team_d != team_m || (team_d == 1 && seg_d != seg_m);
-    }
-    f3s_status s =
-        build_items(p->masked, d_window_offsets, d_window_order, W, H, seg_m, team_m, st);
-    if (s == F3S_OK && p->has_dense)
-        s = build_items(p->dense, d_window_offsets, d_window_order, W, H, seg_d, team_d, st);
+    const f3s_status s = build_plan_sets(p, d_window_offsets, d_window_order, seg_tiles, st);
     if (s != F3S_OK) {
         delete p;
         return s;
@@ -1048,11 +1081,14 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     plan->compiled_block_col = nullptr;
     plan->compiled_n = -1;
     const int64_t ni = plan->masked.num_items;
-    DeviceBuffer counts, tmp;
-    F3S_TRY(counts.reserve(sizeof(int32_t) * (size_t)(ni + 1)));
-    F3S_TRY(tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(ni)));
-    DeviceBuffer base64;
-    F3S_TRY(base64.reserve(sizeof(int64_t) * (size_t)(ni + 1)));
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t cnt_bytes = al(sizeof(int32_t) * (size_t)(ni + 1));
+    const size_t base_bytes = al(sizeof(int64_t) * (size_t)(ni + 1));
+    StreamBuffer buf(st);
+    F3S_TRY(buf.reserve(cnt_bytes + base_bytes + sizeof(int64_t) * (size_t)scan_tmp_elems(ni)));
+    auto* counts = reinterpret_cast<int32_t*>(buf.ptr);
+    auto* b64 = reinterpret_cast<int64_t*>(static_cast<char*>(buf.ptr) + cnt_bytes);
+    auto* tmp = reinterpret_cast<int64_t*>(static_cast<char*>(buf.ptr) + cnt_bytes + base_bytes);
     // the records hold row references: byte offsets, or node indices when the
     // feature tensors are too large for 32-bit offsets (wide launches)
     const bool wide = wide_features(n, plan->H);
@@ -1062,22 +1098,20 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     const dim3 grid((unsigned)ceil_div(ni > 0 ? ni : 1, 4));
     if (ni > 0)
         hipLaunchKernelGGL(plan_columns<false>, grid, dim3(256), 0, st, items, ni, d_block_col,
-                           d_tile_mask, n, ref_stride, no_ref,
-                           reinterpret_cast<int32_t*>(counts.ptr), nullptr, nullptr);
+                           d_tile_mask, n, ref_stride, no_ref, counts, nullptr, nullptr);
     F3S_HIP(hipGetLastError());
-    auto* b64 = reinterpret_cast<int64_t*>(base64.ptr);
-    F3S_TRY(exclusive_scan_i32_to_i64(reinterpret_cast<const int32_t*>(counts.ptr), b64, ni,
-                                      reinterpret_cast<int64_t*>(tmp.ptr), st));
-    int64_t total = 0;
-    F3S_HIP(hipMemcpyAsync(&total, b64 + ni, sizeof total, hipMemcpyDeviceToHost, st));
+    F3S_TRY(exclusive_scan_i32_to_i64(counts, b64, ni, tmp, st));
+    int64_t* h = host_staging();
+    F3S_HIP(hipMemcpyAsync(h, b64 + ni, sizeof(int64_t), hipMemcpyDeviceToHost, st));
     F3S_HIP(hipStreamSynchronize(st));
+    const int64_t total = h[0];
     if (total >= INT32_MAX) {
         set_error("f3s_plan_compile: more than 2^31-1 chunks");
         return F3S_EUNSUPPORTED;
     }
     // four records of padding: the pass reads records in blocks of four
-    F3S_TRY(plan->columns.reserve(sizeof(uint32_t) * 64 * (size_t)(total + 4)));
-    F3S_TRY(plan->chunk_base.reserve(sizeof(int32_t) * (size_t)(ni + 1)));
+    F3S_TRY(plan->columns.reserve(sizeof(uint32_t) * 64 * (size_t)(total + 4), st));
+    F3S_TRY(plan->chunk_base.reserve(sizeof(int32_t) * (size_t)(ni + 1), st));
     if (ni > 0) {
         hipLaunchKernelGGL(plan_columns<true>, grid, dim3(256), 0, st, items, ni, d_block_col,
                            d_tile_mask, n, ref_stride, no_ref, nullptr, b64,
@@ -1087,6 +1121,7 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
     hipLaunchKernelGGL(offsets_to_i32_plan, dim3((unsigned)ceil_div(ni + 1, 256)), dim3(256), 0,
                        st, b64, reinterpret_cast<int32_t*>(plan->chunk_base.ptr), ni + 1);
     F3S_HIP(hipGetLastError());
+    // the lists are complete (and usable on any stream) on return
     F3S_HIP(hipStreamSynchronize(st));
     plan->num_chunks = total;
     plan->compiled_tile_mask = d_tile_mask;
@@ -1097,6 +1132,21 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
 
 f3s_status f3s_plan_destroy(f3s_plan* plan)
 {
+    if (!plan) return F3S_OK;
+    // one wait for the plan's device (its passes may run on any stream), then
+    // every buffer goes back to the allocator's cache at once
+    int dev = plan->masked.items.device, cur = -1;
+    const bool switch_dev = dev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != dev &&
+                            hipSetDevice(dev) == hipSuccess;
+    (void)hipDeviceSynchronize();
+    for (f3s_item_set* set : {&plan->masked, &plan->dense}) {
+        set->items.release_idle();
+        set->splits.release_idle();
+    }
+    plan->partials.release_idle();
+    plan->chunk_base.release_idle();
+    plan->columns.release_idle();
+    if (switch_dev) (void)hipSetDevice(cur);
     delete plan;
     return F3S_OK;
 }
@@ -1109,6 +1159,19 @@ f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_
     if (num_split_windows) *num_split_windows = plan->masked.num_split;
     if (T) *T = plan->T;
     if (seg_tiles) *seg_tiles = plan->masked.seg;
+    return F3S_OK;
+}
+
+f3s_status f3s_plan_stats(const f3s_plan* plan, int64_t* num_chunks, int64_t* masked_items,
+                          int64_t* masked_slots, int64_t* dense_items, int64_t* dense_slots)
+{
+    F3S_REQUIRE(plan != nullptr, "f3s_plan_stats: NULL plan");
+    const f3s_item_set& dense = plan->has_dense ? plan->dense : plan->masked;
+    if (num_chunks) *num_chunks = plan->compiled_n >= 0 ? plan->num_chunks : 0;
+    if (masked_items) *masked_items = plan->masked.num_items;
+    if (masked_slots) *masked_slots = plan->masked.num_slots;
+    if (dense_items) *dense_items = dense.num_items;
+    if (dense_slots) *dense_slots = dense.num_slots;
     return F3S_OK;
 }
 
@@ -1175,7 +1238,7 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
     p.W = plan->W;
     p.n = n;
     p.xcd_contiguous = plan->natural_order;
-    p.partials = reinterpret_cast<float*>(set.partials.ptr);
+    p.partials = reinterpret_cast<float*>(plan->partials.ptr);
     p.splits = reinterpret_cast<const SplitInfo*>(set.splits.ptr);
     p.num_split = set.num_split;
     p.team = set.team;

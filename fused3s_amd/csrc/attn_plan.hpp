@@ -10,7 +10,7 @@ struct f3s_item_set {
     int32_t seg = 0;
     int32_t team = 1;   // > 1: every window is one team of this many items, merged in LDS
     int64_t num_items = 0, num_split = 0, num_slots = 0;
-    f3s::DeviceBuffer items, splits, partials;
+    f3s::DeviceBuffer items, splits;
 };
 
 struct f3s_plan {
@@ -24,6 +24,9 @@ struct f3s_plan {
     // an explicit segment size) they share `masked`.
     f3s_item_set masked, dense;
     bool has_dense = false;
+    // (m, l, O) partials of split-window segments, sized for the set with the
+    // most slots: both sets share it, since a plan serves one pass at a time
+    f3s::DeviceBuffer partials;
     // compiled column lists (f3s_plan_compile) and the structure they describe
     f3s::DeviceBuffer chunk_base, columns;
     const int32_t* compiled_block_col = nullptr;

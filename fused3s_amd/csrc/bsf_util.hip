@@ -79,7 +79,7 @@ f3s_status f3s_window_order(const int32_t* d_window_offsets, int32_t W, int32_t*
     F3S_TRY(require_device());
     clear_error();
     hipStream_t st = as_stream(stream);
-    DeviceBuffer keys_in, keys_out, vals_in, tmp;
+    StreamBuffer keys_in(st), keys_out(st), vals_in(st), tmp(st);
     F3S_TRY(keys_in.reserve(sizeof(uint32_t) * (size_t)W));
     F3S_TRY(keys_out.reserve(sizeof(uint32_t) * (size_t)W));
     F3S_TRY(vals_in.reserve(sizeof(int32_t) * (size_t)W));
@@ -116,7 +116,7 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
     F3S_TRY(require_device());
     clear_error();
     hipStream_t st = as_stream(stream);
-    DeviceBuffer out;
+    StreamBuffer out(st);
     F3S_TRY(out.reserve(2 * sizeof(unsigned long long)));
     F3S_HIP(hipMemsetAsync(out.ptr, 0, 2 * sizeof(unsigned long long), st));
     int64_t blocks = ceil_div(T, 256);

@@ -841,18 +841,66 @@ convert_light(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ c
     if (tid == 0 && *L.bad) atomicOr(err, kErrCol);
 }
 
+// int64 window offsets -> the caller's int32 offsets; thread 0 also reports
+// the error bits and the tile count for the host (status[0], status[1]).
 __global__ void offsets_to_i32(const int64_t* __restrict__ in, int32_t* __restrict__ out,
-                               int64_t count)
+                               int64_t count, const int32_t* __restrict__ err,
+                               int64_t* __restrict__ status)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < count) out[i] = (int32_t)in[i];
+    if (i == 0) {
+        status[0] = *err;
+        status[1] = in[count - 1];
+    }
 }
 
-// Per-call workspace of the converter (counts, scan temporaries, the hub
-// window list, flags: error bits and the hub count).
+// The fill pass's error bits and the tile count it was given (status[0..1]).
+__global__ void fill_status(const int32_t* __restrict__ window_offsets, int32_t W,
+                            const int32_t* __restrict__ err, int64_t* __restrict__ status)
+{
+    if (threadIdx.x == 0) {
+        status[0] = *err;
+        status[1] = window_offsets[W];
+    }
+}
+
+// Per-call workspace of the converter, one pool allocation: status words
+// (error bits, hub count, two int64 results), the hub window list and, for
+// the count pass, the counts, their int64 scan and its temporaries.
 struct ConvertScratch {
-    DeviceBuffer counts, offs64, tmp, hubs, flags;
+    int32_t* err;
+    int32_t* num_hubs;
+    int64_t* status;
+    int32_t* hubs;
+    int32_t* counts;
+    int64_t* offs64;
+    int64_t* tmp;
 };
+
+static f3s_status convert_scratch(StreamBuffer& buf, int32_t W, bool count, ConvertScratch& s)
+{
+    const size_t head = 32;   // err, num_hubs, pad, status[2]
+    const size_t hubs = sizeof(int32_t) * ((size_t)W + 1);
+    const size_t counts = count ? sizeof(int32_t) * (size_t)W : 0;
+    const size_t offs = count ? sizeof(int64_t) * ((size_t)W + 1) : 0;
+    const size_t tmp = count ? sizeof(int64_t) * (size_t)scan_tmp_elems(W) : 0;
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    F3S_TRY(buf.reserve(al(head) + al(hubs) + al(counts) + al(offs) + al(tmp)));
+    char* p = static_cast<char*>(buf.ptr);
+    s.err = reinterpret_cast<int32_t*>(p);
+    s.num_hubs = s.err + 1;
+    s.status = reinterpret_cast<int64_t*>(p + 16);
+    p += al(head);
+    s.hubs = reinterpret_cast<int32_t*>(p);
+    p += al(hubs);
+    s.counts = reinterpret_cast<int32_t*>(p);
+    p += al(counts);
+    s.offs64 = reinterpret_cast<int64_t*>(p);
+    p += al(offs);
+    s.tmp = reinterpret_cast<int64_t*>(p);
+    return F3S_OK;
+}
 
 // One pass (count or fill) over all windows: the persistent kernel with as
 // many workgroups as fit on the device at once, then the hub windows it
@@ -894,34 +942,39 @@ static f3s_status launch_pass(const int32_t* row_ptr, const int32_t* col_idx, in
     return F3S_OK;
 }
 
+// Count call: tile counts, their scan into the caller's offsets, and one
+// host round trip for the error bits and T.  Fill call: the lists, and one
+// round trip for the error bits.
 static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, int32_t n,
                                int64_t nnz, int32_t* window_offsets, int32_t* block_col,
                                uint16_t* tile_mask, int64_t* T_out, hipStream_t stream)
 {
     const int32_t W = (int32_t)ceil_div(n, 16);
+    const bool count = block_col == nullptr;
+    StreamBuffer buf(stream);
     ConvertScratch s;
-    F3S_TRY(s.flags.reserve(sizeof(int32_t) * 2 + sizeof(int64_t)));
-    F3S_TRY(s.hubs.reserve(sizeof(int32_t) * ((size_t)W + 1)));
-    int32_t* err = reinterpret_cast<int32_t*>(s.flags.ptr);
-    int32_t* num_hubs = err + 1;
-    int32_t* hubs = reinterpret_cast<int32_t*>(s.hubs.ptr);
-    F3S_HIP(hipMemsetAsync(err, 0, 2 * sizeof(int32_t), stream));
-
-    if (!block_col) {
-        F3S_TRY(s.counts.reserve(sizeof(int32_t) * (size_t)W));
-        F3S_TRY(s.offs64.reserve(sizeof(int64_t) * ((size_t)W + 1)));
-        F3S_TRY(s.tmp.reserve(sizeof(int64_t) * (size_t)scan_tmp_elems(W)));
-        int32_t* counts = reinterpret_cast<int32_t*>(s.counts.ptr);
-        F3S_TRY(launch_pass<false>(row_ptr, col_idx, n, nnz, W, counts, nullptr, nullptr,
-                                   nullptr, hubs, num_hubs, err, stream));
-        int64_t* offs64 = reinterpret_cast<int64_t*>(s.offs64.ptr);
-        F3S_TRY(exclusive_scan_i32_to_i64(counts, offs64, W,
-                                          reinterpret_cast<int64_t*>(s.tmp.ptr), stream));
-        int32_t h_err = 0;
-        int64_t total = 0;
-        F3S_HIP(hipMemcpyAsync(&h_err, err, sizeof h_err, hipMemcpyDeviceToHost, stream));
-        F3S_HIP(hipMemcpyAsync(&total, offs64 + W, sizeof total, hipMemcpyDeviceToHost, stream));
-        F3S_HIP(hipStreamSynchronize(stream));
+    F3S_TRY(convert_scratch(buf, W, count, s));
+    F3S_HIP(hipMemsetAsync(s.err, 0, 2 * sizeof(int32_t), stream));
+    if (count) {
+        F3S_TRY(launch_pass<false>(row_ptr, col_idx, n, nnz, W, s.counts, nullptr, nullptr,
+                                   nullptr, s.hubs, s.num_hubs, s.err, stream));
+        F3S_TRY(exclusive_scan_i32_to_i64(s.counts, s.offs64, W, s.tmp, stream));
+        hipLaunchKernelGGL(offsets_to_i32, dim3((unsigned)ceil_div(W + 1, 256)), dim3(256), 0,
+                           stream, s.offs64, window_offsets, (int64_t)W + 1, s.err, s.status);
+    } else {
+        F3S_TRY(launch_pass<true>(row_ptr, col_idx, n, nnz, W, nullptr, window_offsets,
+                                  block_col, tile_mask, s.hubs, s.num_hubs, s.err, stream));
+        hipLaunchKernelGGL(fill_status, dim3(1), dim3(64), 0, stream, window_offsets, W, s.err,
+                           s.status);
+    }
+    F3S_HIP(hipGetLastError());
+    int64_t* h = host_staging();
+    F3S_HIP(hipMemcpyAsync(h, s.status, 2 * sizeof(int64_t), hipMemcpyDeviceToHost, stream));
+    F3S_HIP(hipStreamSynchronize(stream));
+    const int32_t h_err = (int32_t)h[0];
+    const int64_t total = h[1];
+    if (count) {
+        // (on an error the offsets written are meaningless, as documented)
         if (h_err & kErrRowPtr) {
             set_error("f3s_convert_csr_to_bsf: row_ptr is not monotone within [0, nnz]");
             return F3S_EDATA;
@@ -934,21 +987,9 @@ static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, i
             set_error("f3s_convert_csr_to_bsf: more than 2^31-1 active tiles");
             return F3S_EUNSUPPORTED;
         }
-        hipLaunchKernelGGL(offsets_to_i32, dim3((unsigned)ceil_div(W + 1, 256)), dim3(256), 0,
-                           stream, offs64, window_offsets, (int64_t)W + 1);
-        F3S_HIP(hipGetLastError());
-        F3S_HIP(hipStreamSynchronize(stream));
         *T_out = total;
         return F3S_OK;
     }
-
-    F3S_TRY(launch_pass<true>(row_ptr, col_idx, n, nnz, W, nullptr, window_offsets, block_col,
-                              tile_mask, hubs, num_hubs, err, stream));
-    int32_t h_err = 0, total = 0;
-    F3S_HIP(hipMemcpyAsync(&h_err, err, sizeof h_err, hipMemcpyDeviceToHost, stream));
-    F3S_HIP(hipMemcpyAsync(&total, window_offsets + W, sizeof total, hipMemcpyDeviceToHost,
-                           stream));
-    F3S_HIP(hipStreamSynchronize(stream));
     if (h_err & (kErrRowPtr | kErrCol)) {
         set_error("f3s_convert_csr_to_bsf: CSR violates the format (row_ptr or column range)");
         return F3S_EDATA;

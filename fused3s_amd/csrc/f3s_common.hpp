@@ -40,16 +40,58 @@ hipError_t warm_attention(hipStream_t s);
 hipError_t warm_bsf_util(hipStream_t s);
 hipError_t warm_naive(hipStream_t s);
 
-// Small grow-only device buffer (per call site).
+// Device memory of the library, from a caching allocator over hipMalloc:
+// freed blocks are kept per device and size class for reuse, so repeated
+// conversions, plans and scratch buffers do not pay the driver's allocation
+// and page-mapping cost each time.  dev_alloc's block is usable on `stream`
+// at once (if it was last used elsewhere, `stream` waits for that use) and
+// on other streams once `stream` has been synchronised.
+f3s_status dev_alloc(void** ptr, size_t bytes, hipStream_t stream);
+// Returns `ptr` for reuse after the work queued on `stream` before this call
+// (stream-ordered); `device` is the device it was allocated on.
+void dev_free(void* ptr, int device, hipStream_t stream);
+// Returns `ptr` for reuse at once: the caller knows no work uses it.
+void dev_free_idle(void* ptr, int device);
+// Waits for every stream of `device`, then returns `ptr` for reuse: for
+// memory whose last users may be on any stream (hipFree's behaviour).
+void dev_free_synced(void* ptr, int device);
+// Host-pinned staging words of the calling thread (16 x int64), for the small
+// device-to-host reads of counts and status that size outputs.
+int64_t* host_staging();
+
+// Grow-only device buffer owned by a long-lived object (a plan): allocated on
+// the owner's stream, which the owner synchronises before handing the buffer
+// out; released after waiting for every stream of its device.
 struct DeviceBuffer {
     void* ptr = nullptr;
     size_t bytes = 0;
-    f3s_status reserve(size_t want);
+    int device = -1;
+    f3s_status reserve(size_t want, hipStream_t stream);
     void release();
+    void release_idle();   // the owner has synchronised the device
     DeviceBuffer() = default;
     DeviceBuffer(const DeviceBuffer&) = delete;              // owns its allocation
     DeviceBuffer& operator=(const DeviceBuffer&) = delete;
     ~DeviceBuffer() { release(); }
+};
+
+// Scratch memory of one call: allocated on the call's stream and returned to
+// the pool in stream order when it goes out of scope, so a call that queues
+// work on the stream and returns without waiting may still use it on the
+// device.  The stream must outlive the object (it does for call-local use).
+struct StreamBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    explicit StreamBuffer(hipStream_t s) : stream(s) {}
+    f3s_status reserve(size_t want);
+    StreamBuffer(const StreamBuffer&) = delete;
+    StreamBuffer& operator=(const StreamBuffer&) = delete;
+    ~StreamBuffer()
+    {
+        if (ptr) dev_free(ptr, device, stream);
+    }
 };
 
 }  // namespace f3s

@@ -329,11 +329,11 @@ static int32_t load_impl(const char* path, int32_t* n_out, int64_t* nnz_out,
         const int32_t* wo = (const int32_t*)arr[2];
         const int32_t* bc = (const int32_t*)arr[3];
         if (wo[0] != 0 || wo[W] != T) bad = "window_offsets must run from 0 to T";
+        // The whole offset array first: monotone from 0 to T puts every entry
+        // in [0, T], so the block-column walk below stays inside block_col.
+        for (int64_t w = 0; bad.empty() && w < W; ++w)
+            if (wo[w + 1] < wo[w]) bad = "window_offsets is not monotone";
         for (int64_t w = 0; bad.empty() && w < W; ++w) {
-            if (wo[w + 1] < wo[w]) {
-                bad = "window_offsets is not monotone";
-                break;
-            }
             for (int64_t t = wo[w]; t < wo[w + 1]; ++t)
                 if (bc[t] < 0 || bc[t] >= W || (t > wo[w] && bc[t] <= bc[t - 1])) {
                     bad = "block columns must ascend within [0, W) in each window";

@@ -2,7 +2,12 @@
 // device-wide scan used by the converter and the planner.
 #include <stdio.h>
 
+#include <iterator>
+#include <map>
+#include <mutex>
 #include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "f3s_common.hpp"
 #include "f3s_device.hpp"
@@ -43,21 +48,246 @@ f3s_status require_device()
     return F3S_OK;
 }
 
-f3s_status DeviceBuffer::reserve(size_t want)
+// ------------------------------------------------------------ device memory
+//
+// A caching allocator over hipMalloc.  Freed blocks go to a per-device cache
+// keyed by size class instead of back to the driver, whose large allocations
+// and frees cost 0.05-1.7 ms each on MI355X (page mapping; ROCm's
+// stream-ordered pools measured no better for large blocks, their frees
+// unmapping the memory).  A block freed in stream order carries an event
+// recorded on its stream at the free; whoever takes it next waits for that
+// event (on the device, through its own stream), so a block is never reused
+// while its last user's work may still run.  Idle cached bytes are capped per
+// device; on an allocation failure the cache is returned to the driver and
+// the allocation retried.
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+constexpr size_t kSmallQuantum = 512;
+constexpr size_t kLargeQuantum = (size_t)2 << 20;
+constexpr size_t kCacheCap = (size_t)16 << 30;   // idle cached bytes kept per device
+
+struct CachedBlock {
+    void* ptr;
+    hipEvent_t last_use;   // recorded where the block was freed (nullptr: no pending use)
+};
+
+struct DeviceCache {
+    std::multimap<size_t, CachedBlock> idle;   // by size
+    std::unordered_map<void*, size_t> live;    // blocks handed out, and their sizes
+    std::vector<hipEvent_t> spare_events;
+    size_t idle_bytes = 0;
+};
+
+std::mutex g_mem_mu;
+DeviceCache g_cache[kMaxDevices];
+
+size_t size_class(size_t bytes)
+{
+    if (bytes < kLargeQuantum / 2) return (bytes + kSmallQuantum - 1) / kSmallQuantum * kSmallQuantum;
+    return (bytes + kLargeQuantum - 1) / kLargeQuantum * kLargeQuantum;
+}
+
+// Frees one idle block to the driver (its last use must be complete).
+void drop_block(DeviceCache& c, void* ptr, hipEvent_t ev)
+{
+    if (ev) {
+        (void)hipEventSynchronize(ev);
+        c.spare_events.push_back(ev);
+    }
+    (void)hipFree(ptr);
+}
+
+// Returns every idle block of the current device `dev` to the driver.
+void drop_idle(DeviceCache& c)
+{
+    for (auto& kv : c.idle) drop_block(c, kv.second.ptr, kv.second.last_use);
+    c.idle.clear();
+    c.idle_bytes = 0;
+}
+
+void cache_idle(DeviceCache& c, void* ptr, size_t size, hipEvent_t ev)
+{
+    c.idle.emplace(size, CachedBlock{ptr, ev});
+    c.idle_bytes += size;
+    // over the cap: the largest idle blocks go back to the driver
+    while (c.idle_bytes > kCacheCap && !c.idle.empty()) {
+        auto it = std::prev(c.idle.end());
+        c.idle_bytes -= it->first;
+        drop_block(c, it->second.ptr, it->second.last_use);
+        c.idle.erase(it);
+    }
+}
+
+}  // namespace
+
+f3s_status dev_alloc(void** ptr, size_t bytes, hipStream_t stream)
+{
+    *ptr = nullptr;
+    const size_t size = size_class(bytes ? bytes : 1);
+    int dev = 0;
+    F3S_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) {
+        F3S_HIP(hipMalloc(ptr, size));
+        return F3S_OK;
+    }
+    std::lock_guard<std::mutex> lock(g_mem_mu);
+    DeviceCache& c = g_cache[dev];
+    // a cached block of this size class, or a close larger one (at most a
+    // quarter, plus one quantum, bigger)
+    auto it = c.idle.lower_bound(size);
+    if (it != c.idle.end() && it->first <= size + size / 4 + kLargeQuantum) {
+        const size_t got = it->first;
+        const CachedBlock b = it->second;
+        c.idle.erase(it);
+        c.idle_bytes -= got;
+        if (b.last_use) {
+            const hipError_t q = hipEventQuery(b.last_use);
+            if (q != hipSuccess) {
+                (void)hipGetLastError();   // not ready: the new user's stream waits for it
+                const hipError_t w = hipStreamWaitEvent(stream, b.last_use, 0);
+                if (w != hipSuccess) {
+                    c.idle.emplace(got, b);
+                    c.idle_bytes += got;
+                    return hip_fail(w, "hipStreamWaitEvent", __FILE__, __LINE__);
+                }
+            }
+            c.spare_events.push_back(b.last_use);
+        }
+        c.live[b.ptr] = got;
+        *ptr = b.ptr;
+        return F3S_OK;
+    }
+    hipError_t e = hipMalloc(ptr, size);
+    if (e == hipErrorOutOfMemory) {
+        (void)hipGetLastError();
+        drop_idle(c);
+        e = hipMalloc(ptr, size);
+    }
+    if (e != hipSuccess) {
+        *ptr = nullptr;
+        return hip_fail(e, "hipMalloc", __FILE__, __LINE__);
+    }
+    c.live[*ptr] = size;
+    return F3S_OK;
+}
+
+void dev_free(void* ptr, int device, hipStream_t stream)
+{
+    if (!ptr) return;
+    if (device < 0 || device >= kMaxDevices) {
+        (void)hipFree(ptr);
+        return;
+    }
+    std::lock_guard<std::mutex> lock(g_mem_mu);
+    DeviceCache& c = g_cache[device];
+    auto it = c.live.find(ptr);
+    if (it == c.live.end()) {   // not ours: the driver's
+        (void)hipFree(ptr);
+        return;
+    }
+    const size_t size = it->second;
+    c.live.erase(it);
+    hipEvent_t ev = nullptr;
+    if (!c.spare_events.empty()) {
+        ev = c.spare_events.back();
+        c.spare_events.pop_back();
+    } else if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        ev = nullptr;
+    }
+    if (!ev || hipEventRecord(ev, stream) != hipSuccess) {
+        // no event to order the reuse by: wait for the stream instead
+        (void)hipGetLastError();
+        (void)hipStreamSynchronize(stream);
+        if (ev) c.spare_events.push_back(ev);
+        ev = nullptr;
+    }
+    cache_idle(c, ptr, size, ev);
+}
+
+void dev_free_idle(void* ptr, int device)
+{
+    if (!ptr) return;
+    if (device < 0 || device >= kMaxDevices) {
+        (void)hipFree(ptr);
+        return;
+    }
+    std::lock_guard<std::mutex> lock(g_mem_mu);
+    DeviceCache& c = g_cache[device];
+    auto it = c.live.find(ptr);
+    if (it == c.live.end()) {
+        (void)hipFree(ptr);
+        return;
+    }
+    const size_t size = it->second;
+    c.live.erase(it);
+    cache_idle(c, ptr, size, nullptr);
+}
+
+void dev_free_synced(void* ptr, int device)
+{
+    if (!ptr) return;
+    int cur = -1;
+    const bool switch_dev = hipGetDevice(&cur) == hipSuccess && device >= 0 && cur != device &&
+                            hipSetDevice(device) == hipSuccess;
+    (void)hipDeviceSynchronize();
+    dev_free_idle(ptr, device);
+    if (switch_dev) (void)hipSetDevice(cur);
+}
+
+int64_t* host_staging()
+{
+    thread_local int64_t* words = nullptr;   // one small pinned block per host thread
+    if (!words) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, 16 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            thread_local int64_t fallback[16];
+            return fallback;   // pageable: correct, only slower to copy into
+        }
+        words = static_cast<int64_t*>(p);
+    }
+    return words;
+}
+
+f3s_status DeviceBuffer::reserve(size_t want, hipStream_t stream)
 {
     if (want <= bytes && ptr) return F3S_OK;
     release();
     size_t alloc = want ? want : 1;
-    F3S_HIP(hipMalloc(&ptr, alloc));
+    F3S_HIP(hipGetDevice(&device));
+    F3S_TRY(dev_alloc(&ptr, alloc, stream));
     bytes = alloc;
     return F3S_OK;
 }
 
 void DeviceBuffer::release()
 {
-    if (ptr) (void)hipFree(ptr);
+    if (ptr) dev_free_synced(ptr, device);
     ptr = nullptr;
     bytes = 0;
+}
+
+void DeviceBuffer::release_idle()
+{
+    if (ptr) dev_free_idle(ptr, device);
+    ptr = nullptr;
+    bytes = 0;
+}
+
+f3s_status StreamBuffer::reserve(size_t want)
+{
+    if (want <= bytes && ptr) return F3S_OK;
+    if (ptr) dev_free(ptr, device, stream);
+    ptr = nullptr;
+    bytes = 0;
+    size_t alloc = want ? want : 1;
+    F3S_HIP(hipGetDevice(&device));
+    F3S_TRY(dev_alloc(&ptr, alloc, stream));
+    bytes = alloc;
+    return F3S_OK;
 }
 
 // ------------------------------------------------------------------ scan
@@ -244,14 +474,52 @@ f3s_status f3s_malloc(void** ptr, uint64_t bytes)
     F3S_REQUIRE(ptr != nullptr, "f3s_malloc: ptr is NULL");
     *ptr = nullptr;
     F3S_TRY(require_device());
-    F3S_HIP(hipMalloc(ptr, bytes ? bytes : 1));
+    // from the device's pool, then usable on every stream (as hipMalloc's memory)
+    F3S_TRY(dev_alloc(ptr, bytes, nullptr));
+    const hipError_t e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        dev_free_synced(*ptr, dev);
+        *ptr = nullptr;
+        return hip_fail(e, "hipStreamSynchronize", __FILE__, __LINE__);
+    }
     return F3S_OK;
 }
 
 f3s_status f3s_free(void* ptr)
 {
     if (!ptr) return F3S_OK;
-    F3S_HIP(hipFree(ptr));
+    int dev = 0;
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, ptr) == hipSuccess) {
+        dev = attr.device;
+    } else {
+        (void)hipGetLastError();
+        F3S_HIP(hipGetDevice(&dev));
+    }
+    // as hipFree: waits for the device, so no stream still uses the memory
+    dev_free_synced(ptr, dev);
+    return F3S_OK;
+}
+
+f3s_status f3s_release_cached_memory(void)
+{
+    int count = 0, cur = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || hipGetDevice(&cur) != hipSuccess) {
+        (void)hipGetLastError();
+        return F3S_OK;   // nothing was allocated
+    }
+    std::lock_guard<std::mutex> lock(g_mem_mu);
+    for (int d = 0; d < count && d < kMaxDevices; ++d) {
+        DeviceCache& c = g_cache[d];
+        if (c.idle.empty() && c.spare_events.empty()) continue;
+        F3S_HIP(hipSetDevice(d));
+        drop_idle(c);
+        for (hipEvent_t ev : c.spare_events) (void)hipEventDestroy(ev);
+        c.spare_events.clear();
+        (void)hipSetDevice(cur);
+    }
     return F3S_OK;
 }
 

@@ -20,7 +20,9 @@
  *                  style buffer padded to 16W rows also works).
  *
  * Thread safety: calls on different streams may run concurrently; the
- * library keeps no mutable global state besides the per-thread last error.
+ * library's only mutable global state is the per-thread last error and the
+ * per-device memory pools (set up once under a lock; the pool API is
+ * thread-safe).
  * A plan owns the partial-result buffers of its split windows, so one plan
  * must not serve two overlapping calls.
  */
@@ -65,8 +67,17 @@ f3s_status f3s_init(void);
 f3s_status f3s_device_count(int32_t* count);
 f3s_status f3s_set_device(int32_t device);
 f3s_status f3s_device_name(char* buf, int32_t buflen);
+/* Device memory comes from a stream-ordered pool per device that keeps freed
+ * memory for reuse, so repeated allocations (of conversion outputs, plans,
+ * scratch) skip the driver's allocation and page mapping.  f3s_malloc'd
+ * memory is usable on every stream on return; f3s_free waits for the device
+ * first, as hipFree does. */
 f3s_status f3s_malloc(void** ptr, uint64_t bytes);
 f3s_status f3s_free(void* ptr);
+/* Returns the memory the pools keep for reuse to the driver (waits for every
+ * device first).  No reference counterpart; for processes that share the GPU
+ * with another allocator, e.g. torch's. */
+f3s_status f3s_release_cached_memory(void);
 f3s_status f3s_memcpy_h2d(void* dst, const void* src, uint64_t bytes, void* stream);
 f3s_status f3s_memcpy_d2h(void* dst, const void* src, uint64_t bytes, void* stream);
 f3s_status f3s_memcpy_d2d(void* dst, const void* src, uint64_t bytes, void* stream);
@@ -90,7 +101,9 @@ f3s_status f3s_cast_f32_to_f16(const float* d_in, uint16_t* d_out, int64_t count
  * non-NULL the 16 row masks of each tile (T*16 entries).  Typical use is two
  * calls: sizes first (d_block_col = NULL), then the lists.  Output is
  * bit-exact with the reference converter.  F3S_EDATA if row_ptr is not
- * monotone from 0 to nnz or a column is outside [0, n). */
+ * monotone from 0 to nnz or a column is outside [0, n) (the offsets written
+ * are then meaningless).  Each call makes one host round trip (to read T and
+ * the error bits); scratch comes from the library's pool. */
 f3s_status f3s_convert_csr_to_bsf(const int32_t* d_row_ptr, const int32_t* d_col_idx,
                                   int32_t n, int64_t nnz,
                                   int32_t* d_window_offsets, int32_t* d_block_col,
@@ -125,9 +138,10 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * launch of their own before the others; in natural order, the first 512
  * windows of more than max(1024, 8 x mean) tiles run as teams of 16 and the
  * first 4,096 of more than max(512, 2 x mean) (but not more than the first
- * bound) as teams of 4, listed by two small kernels into scratch allocated and
- * freed stream-ordered on `stream` (hipMallocAsync / hipFreeAsync).  Every
- * other path allocates nothing. */
+ * bound) as teams of 4, listed by two small kernels into a few tens of KB of
+ * scratch taken from the library's pool and returned to it in stream order
+ * on `stream` (the call does not wait).  Every other path allocates
+ * nothing. */
 f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                              float* O, const int32_t* d_window_offsets,
                              const int32_t* d_block_col, const uint16_t* d_tile_mask,
@@ -181,6 +195,14 @@ f3s_status f3s_plan_compile(f3s_plan* plan, const int32_t* d_block_col,
                             const uint16_t* d_tile_mask, int32_t n, void* stream);
 f3s_status f3s_plan_info(const f3s_plan* plan, int64_t* num_items, int64_t* num_split_windows,
                          int64_t* T, int32_t* seg_tiles);
+/* The sizes behind a planned pass's memory traffic (no reference
+ * counterpart): compiled column chunks (256 bytes each; 0 before
+ * f3s_plan_compile), and for the item sets of masked and of tile-dense
+ * passes their work items (16 bytes each) and split-window partial slots
+ * (per head, 4,224 bytes written by the pass and read by its merge).  Any
+ * output pointer may be NULL. */
+f3s_status f3s_plan_stats(const f3s_plan* plan, int64_t* num_chunks, int64_t* masked_items,
+                          int64_t* masked_slots, int64_t* dense_items, int64_t* dense_slots);
 f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q,
                                      const uint16_t* K, const uint16_t* V, float* O,
                                      const int32_t* d_block_col, const uint16_t* d_tile_mask,

@@ -125,6 +125,24 @@ def test_invalid_contents_are_rejected(tmp_path):
         f3s.load_graph(p)
 
 
+@pytest.mark.parametrize("k", [1, 50, 100000])
+def test_offsets_past_the_tile_count_are_rejected(tmp_path, k):
+    # window_offsets = [0, T + k, ..., T]: an entry past T must be rejected
+    # before any block column is read through it (the block_col array holds
+    # exactly T entries), with a valid checksum in front of it.
+    rp, ci = random_csr(64, 4, 7)
+    bsf = oracle_bsf(rp, ci)
+    T = int(bsf.window_offsets[-1])
+    wo = bsf.window_offsets.copy()
+    assert len(wo) >= 3
+    wo[1] = T + k
+    p = str(tmp_path / "o.f3sg")
+    f3s.save_graph(p, rp, ci, f3s.BlockSparseFormat(bsf.num_row_windows, wo,
+                                                    bsf.block_col_indices, bsf.tile_masks))
+    with pytest.raises(RuntimeError, match="not monotone"):
+        f3s.load_graph(p)
+
+
 def test_writer_rejects_wrong_window_count(tmp_path):
     rp, ci = random_csr(40, 4, 6)
     bsf = oracle_bsf(rp, ci)
