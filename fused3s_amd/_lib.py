@@ -48,6 +48,8 @@ HIP_API = {
     "f3s_bsf_stats": (c_i32, [c_vp, c_vp, c_i64, c_i32, P_i64, P_i64, c_vp]),
     "f3s_attention_fwd": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                   c_i32, c_i32, c_i32, c_i32, c_f32, c_vp]),
+    "f3s_attention_fwd_noalloc": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                          c_i32, c_i32, c_i32, c_i32, c_f32, c_vp]),
     "f3s_attention_fwd_timed": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                         c_i32, c_i32, c_i32, c_i32, c_f32, c_vp, c_i32,
                                         C.POINTER(c_f32)]),

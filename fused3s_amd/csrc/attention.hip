@@ -46,6 +46,7 @@
 // code relies only on that and on the row/column/C mapping.
 #include <algorithm>
 #include <math.h>
+#include <mutex>
 #include <new>
 #include <stdio.h>
 
@@ -926,17 +927,25 @@ static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
     return F3S_OK;
 }
 
-}  // namespace f3s
+// Bytes of the natural-order launch's scratch for W windows: the two heavy
+// window lists, two per-block counts per 256 windows and the bitmap of the
+// listed windows.
+static size_t natural_scratch_bytes(int64_t W)
+{
+    const int64_t nb = ceil_div(W, 256), words = ceil_div(W, 32);
+    return sizeof(int32_t) * ((size_t)kHeavyMaxWindows + kHeavyMaxWindowsNat + 2 * (size_t)nb) +
+           sizeof(uint32_t) * (size_t)words;
+}
 
-using namespace f3s;
-
-extern "C" {
-
-f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,
-                             const int32_t* d_window_offsets, const int32_t* d_block_col,
-                             const uint16_t* d_tile_mask, const int32_t* d_window_order,
-                             int32_t W, int32_t n, int32_t d, int32_t H, float scale,
-                             void* stream)
+// f3s_attention_fwd; the natural-order launch takes its scratch from
+// `fixed_scratch` when given (f3s_attention_fwd_noalloc, already checked to
+// be large enough), else from the allocator, returned in stream order.
+static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                                     float* O, const int32_t* d_window_offsets,
+                                     const int32_t* d_block_col, const uint16_t* d_tile_mask,
+                                     const int32_t* d_window_order, int32_t W, int32_t n,
+                                     int32_t d, int32_t H, float scale, void* stream,
+                                     void* fixed_scratch)
 {
     F3S_TRY(check_attention_args(Q, K, V, O, n, d, H));
     F3S_REQUIRE(W == (int32_t)ceil_div(n, 16), "f3s_attention_fwd: W must equal ceil(n/16)");
@@ -964,18 +973,20 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
         // Natural order: the hubs can be anywhere.  Two small kernels list the
         // large windows (the ordered rule) for teams of 16 and the medium ones
         // for teams of 4 (a 16-wave team holds a CU's LDS, 4 waves a quarter
-        // of it), in a few tens of KB of stream-ordered scratch; one wave each
-        // takes the rest, skipping the listed windows.
+        // of it), in a few tens of KB of scratch; one wave each takes the
+        // rest, skipping the listed windows.
         const HeavyClass large{kHeavyMinTiles, kHeavyMeanFactor, 0, 0, kHeavyMaxWindows};
         const HeavyClass medium{kHeavyMinTilesNat, kHeavyMeanFactorNat, kHeavyMinTiles,
                                 kHeavyMeanFactor, kHeavyMaxWindowsNat};
         const int32_t nb = (int32_t)ceil_div(W, 256);
-        const size_t words = (size_t)ceil_div(W, 32);
-        const size_t bytes = sizeof(int32_t) * ((size_t)large.cap + medium.cap + 2 * (size_t)nb) +
-                             sizeof(uint32_t) * words;
-        StreamBuffer scratch(st);   // returned to the pool in stream order, after the launches
-        F3S_TRY(scratch.reserve(bytes));
-        int32_t* list_l = reinterpret_cast<int32_t*>(scratch.ptr);
+        // every word of it is written by heavy_count before it is read
+        StreamBuffer scratch(st);   // returned to the allocator in stream order, after the launches
+        void* sp = fixed_scratch;
+        if (!sp) {
+            F3S_TRY(scratch.reserve(natural_scratch_bytes(W)));
+            sp = scratch.ptr;
+        }
+        int32_t* list_l = reinterpret_cast<int32_t*>(sp);
         int32_t* list_m = list_l + large.cap;
         int32_t* counts = list_m + medium.cap;   // 2 x nb
         uint32_t* listed = reinterpret_cast<uint32_t*>(counts + 2 * nb);
@@ -1029,6 +1040,100 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
         p.heavy_factor = kHeavyMeanFactor;
     }
     return launch(p, H, scale, st);
+}
+
+
+// ------------------------------------------------ allocation-free entry point
+//
+// f3s_attention_fwd_noalloc: the natural-order launch's scratch (heavy
+// window lists, per-block counts, bitmap) lives in a file-scope device array
+// sized for graphs of up to kNoAllocMaxWindows row windows; each device holds
+// its own copy for the life of the process.  Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device
+// address): its device address is looked up once per device with
+// hipGetSymbolAddress and kept in g_noalloc_addr.
+constexpr int32_t kNoAllocMaxWindows = 1 << 22;   // n <= 67,108,864 nodes
+constexpr size_t kNoAllocScratchBytes =
+    (sizeof(int32_t) * ((size_t)kHeavyMaxWindows + kHeavyMaxWindowsNat +
+                        2 * (((size_t)kNoAllocMaxWindows + 255) / 256)) +
+     sizeof(uint32_t) * (((size_t)kNoAllocMaxWindows + 31) / 32) + 255) / 256 * 256;
+static __device__ __align__(256) unsigned char noalloc_scratch[kNoAllocScratchBytes];
+
+constexpr int kNoAllocDevices = 64;
+static std::mutex g_noalloc_mu;
+static void* g_noalloc_addr[kNoAllocDevices] = {};
+
+// The device address of noalloc_scratch on the current device (looked up on
+// the first call per device, with that device current).
+static f3s_status noalloc_scratch_addr(void** out)
+{
+    *out = nullptr;
+    int dev = 0;
+    F3S_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kNoAllocDevices) {
+        set_error("f3s_attention_fwd_noalloc: device index beyond the library's table");
+        return F3S_EUNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_addr[dev]) {
+        void* p = nullptr;
+        F3S_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch)));
+        if (!p) {
+            set_error("f3s_attention_fwd_noalloc: no device address for its scratch");
+            return F3S_EHIP;
+        }
+        g_noalloc_addr[dev] = p;
+    }
+    *out = g_noalloc_addr[dev];
+    return F3S_OK;
+}
+
+// f3s_init: the current device's address, looked up ahead of the first call.
+f3s_status noalloc_setup()
+{
+    void* p = nullptr;
+    return noalloc_scratch_addr(&p);
+}
+
+}  // namespace f3s
+
+using namespace f3s;
+
+extern "C" {
+
+f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, float* O,
+                             const int32_t* d_window_offsets, const int32_t* d_block_col,
+                             const uint16_t* d_tile_mask, const int32_t* d_window_order,
+                             int32_t W, int32_t n, int32_t d, int32_t H, float scale,
+                             void* stream)
+{
+    return attention_fwd_impl(Q, K, V, O, d_window_offsets, d_block_col, d_tile_mask,
+                              d_window_order, W, n, d, H, scale, stream, nullptr);
+}
+
+f3s_status f3s_attention_fwd_noalloc(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                                     float* O, const int32_t* d_window_offsets,
+                                     const int32_t* d_block_col, const uint16_t* d_tile_mask,
+                                     const int32_t* d_window_order, int32_t W, int32_t n,
+                                     int32_t d, int32_t H, float scale, void* stream)
+{
+    if (W < 0 || W > kNoAllocMaxWindows) {
+        set_error("f3s_attention_fwd_noalloc: W outside [0, 4194304] (the limit of its fixed "
+                  "scratch, graphs of up to 67,108,864 nodes); use f3s_attention_fwd");
+        return F3S_EUNSUPPORTED;
+    }
+    F3S_TRY(check_attention_args(Q, K, V, O, n, d, H));
+    F3S_TRY(require_device());
+    void* sp = nullptr;
+    F3S_TRY(noalloc_scratch_addr(&sp));
+    static_assert(kNoAllocScratchBytes >= sizeof(int32_t) * (kHeavyMaxWindows + kHeavyMaxWindowsNat),
+                  "scratch holds the lists");
+    if (natural_scratch_bytes(W) > kNoAllocScratchBytes) {   // cannot happen for W <= max
+        set_error("f3s_attention_fwd_noalloc: scratch too small");
+        return F3S_EUNSUPPORTED;
+    }
+    return attention_fwd_impl(Q, K, V, O, d_window_offsets, d_block_col, d_tile_mask,
+                              d_window_order, W, n, d, H, scale, stream, sp);
 }
 
 f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_window_order,

@@ -39,6 +39,9 @@ hipError_t warm_convert(hipStream_t s);
 hipError_t warm_attention(hipStream_t s);
 hipError_t warm_bsf_util(hipStream_t s);
 hipError_t warm_naive(hipStream_t s);
+// Looks up the current device's address of f3s_attention_fwd_noalloc's
+// fixed scratch (attention.hip), so its first call does not.
+f3s_status noalloc_setup();
 
 // Device memory of the library, from a caching allocator over hipMalloc:
 // freed blocks are kept per device and size class for reuse, so repeated

@@ -429,6 +429,7 @@ f3s_status f3s_init(void)
     F3S_HIP(warm_bsf_util(nullptr));
     F3S_HIP(warm_naive(nullptr));
     F3S_HIP(hipDeviceSynchronize());
+    F3S_TRY(noalloc_setup());
     return F3S_OK;
 }
 

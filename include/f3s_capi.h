@@ -148,6 +148,23 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
                              const int32_t* d_window_order, int32_t W, int32_t n,
                              int32_t d, int32_t H, float scale, void* stream);
 
+/* f3s_attention_fwd without any device allocation.  No counterpart in the
+ * reference: for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * semantics, kernels and results (bit for bit) as f3s_attention_fwd; the
+ * natural-order launch's scratch (heavy-window lists, per-block counts and a
+ * bitmap: 0.66 MB) is a fixed device array of the library, one per GPU, held
+ * until the process ends.  Limit: W <= 4,194,304 row windows (n <= 67,108,864
+ * nodes); larger W returns F3S_EUNSUPPORTED.  Every call on one GPU shares
+ * that GPU's array and overwrites it, so calls that overlap in time on one
+ * GPU (e.g. on two streams) race; serialise them.  Allocates nothing and
+ * never waits for the device. */
+f3s_status f3s_attention_fwd_noalloc(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                                     float* O, const int32_t* d_window_offsets,
+                                     const int32_t* d_block_col, const uint16_t* d_tile_mask,
+                                     const int32_t* d_window_order, int32_t W, int32_t n,
+                                     int32_t d, int32_t H, float scale, void* stream);
+
 /* The timed launch of tests/test_fused_3s_v2.cu:126-136 (events recorded
  * around the kernel on the launch stream): `reps` back-to-back calls of
  * f3s_attention_fwd with the same arguments, timed with HIP events on
