@@ -4,8 +4,10 @@ Bars: converter tile lists, masks, window order and the fp16 cast are
 bit-exact; attention output has max abs error <= 2e-3 and normwise max
 relative error max|g - c| / max|c| <= 1e-2 against the fp32 oracle on
 identical fp16-rounded inputs.  At the full
-sizes of configs 4 and 5 the oracle checks a deterministic sample of rows
-(including the heaviest windows) and the converter is compared in full.
+sizes of configs 4 and 5 the converter is compared in full and masked
+attention on every row; tile-dense attention on every row of config 4 and
+on a deterministic sample of row ranges (including the heaviest windows) of
+config 5.
 """
 from __future__ import annotations
 
@@ -676,8 +678,52 @@ def sample_rows(bsf_host, n, extra_windows=8, stride_rows=4000, seed=0):
     return ranges
 
 
+def oracle_threads() -> int:
+    """Host threads for whole-graph oracle runs (a one-GPU box's CPU share)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def errors_chunked(got: np.ndarray, want: np.ndarray, chunk: int = 1 << 24) -> tuple[float, float]:
+    """errors() over large arrays in bounded memory: max |g - c| (float64)
+    and that over max |c|."""
+    g, w = got.reshape(-1), want.reshape(-1)
+    mabs, scale = 0.0, 0.0
+    for i in range(0, g.size, chunk):
+        gi = g[i:i + chunk].astype(np.float64)
+        wi = w[i:i + chunk].astype(np.float64)
+        mabs = max(mabs, float(np.abs(gi - wi).max()))
+        scale = max(scale, float(np.abs(wi).max()))
+    return mabs, (mabs / scale if scale > 0 else mabs)
+
+
+def check_whole_graph(what: str, got: np.ndarray, want: np.ndarray) -> None:
+    assert np.all(np.isfinite(got)), f"{what}: unwritten or non-finite rows"
+    mabs, mrel = errors_chunked(got, want)
+    log(f"  {what}: every row, max_abs={mabs:.3e} max_rel={mrel:.3e}")
+    assert mabs <= ABS_TOL and mrel <= REL_TOL, f"{what}: {mabs} {mrel}"
+
+
+def check_sampled(what, got, ranges, want_rows) -> None:
+    assert np.all(np.isfinite(got)), f"{what}: unwritten or non-finite rows"
+    worst = (0.0, 0.0)
+    for (a, b) in ranges:
+        mabs, mrel = errors(got[a:b], want_rows(a, b))
+        assert mabs <= ABS_TOL and mrel <= REL_TOL, f"{what} rows {a}:{b}: {mabs} {mrel}"
+        worst = (max(worst[0], mabs), max(worst[1], mrel))
+    log(f"  {what}: {len(ranges)} row ranges, worst max_abs={worst[0]:.3e} "
+        f"max_rel={worst[1]:.3e}")
+
+
 @pytest.mark.slow
 def test_config4_full_size(gpu):
+    """Config 4 at full size: the converter in full; masked attention on every
+    row (the oracle of baselines/cpu_baseline.cpp:16-91 over the whole graph,
+    as tests/test_fused_3s_v2.cu:141-153 compares every row) for the plan,
+    the compiled plan and the drop-in launch in the reference's descending
+    order and in natural order; tile-dense attention (the reference kernel's
+    semantics, tests/test_fused_3s_v2.cu:17-59: about a TFLOP of tile work
+    for the CPU oracle) on every row for the plan and the drop-in launch in
+    descending order."""
     c = gpu.CONFIGS[4]
     t0 = time.time()
     rp, ci = c.graph()
@@ -693,33 +739,49 @@ def test_config4_full_size(gpu):
     dO = gpu.DeviceArray((n, 1, 64), np.float32)
     order = gpu.window_order_device(bsf)
     hb = bsf.to_host()
-    ranges = sample_rows(hb, n)
     plan = gpu.Plan(bsf, order, H=1)
     log(f"cfg4 plan: items={plan.num_items} split={plan.num_split} seg={plan.seg_tiles}")
     cplan = gpu.Plan(bsf, order, H=1)
     cplan.compile()
-    for masked, pl in ((True, plan), (True, cplan), (False, plan)):
-        dO.fill_bytes(0xFF)
-        pl.forward(dQ, dK, dV, dO, masked=masked)
+
+    def run(fn):
+        dO.fill_bytes(0xFF)   # NaN poison: every row must be written
+        fn()
         gpu.synchronize()
-        got = dO.numpy()
-        assert np.all(np.isfinite(got)), "unwritten or non-finite rows"
-        worst = (0.0, 0.0)
-        for (a, b) in ranges:
-            if masked:
-                want = orc.masked_attention(n, 64, 1, Qf, Kf, Vf, rp, ci, 1.0, a, b)[a:b]
-            else:
-                want = orc.tile_dense_attention(n, 64, 1, Qf, Kf, Vf, hb.window_offsets,
-                                                hb.block_col_indices, 1.0, a, b)[a:b]
-            mabs, mrel = errors(got[a:b], want)
-            assert mabs <= ABS_TOL and mrel <= REL_TOL, f"rows {a}:{b} masked={masked}: {mabs} {mrel}"
-            worst = (max(worst[0], mabs), max(worst[1], mrel))
-        log(f"cfg4 masked={masked}: {len(ranges)} row ranges within tolerance, "
-            f"worst max_abs={worst[0]:.3e} max_rel={worst[1]:.3e}")
+        return dO.numpy()
+
+    th = oracle_threads()
+    t0 = time.time()
+    want = orc.masked_attention(n, 64, 1, Qf, Kf, Vf, rp, ci, 1.0, threads=th)
+    log(f"cfg4 masked oracle, whole graph: {time.time()-t0:.2f}s on {th} threads")
+    masked_runs = [
+        ("plan", lambda: plan.forward(dQ, dK, dV, dO, masked=True)),
+        ("compiled plan", lambda: cplan.forward(dQ, dK, dV, dO, masked=True)),
+        ("drop-in, descending order",
+         lambda: gpu.attention_fwd(dQ, dK, dV, dO, bsf, order, masked=True)),
+        ("drop-in, natural order",
+         lambda: gpu.attention_fwd(dQ, dK, dV, dO, bsf, None, masked=True)),
+    ]
+    for what, fn in masked_runs:
+        check_whole_graph(f"cfg4 masked {what}", run(fn), want)
+    del want
+    t0 = time.time()
+    want = orc.tile_dense_attention(n, 64, 1, Qf, Kf, Vf, hb.window_offsets,
+                                    hb.block_col_indices, 1.0, threads=th)
+    log(f"cfg4 tile-dense oracle, whole graph: {time.time()-t0:.2f}s on {th} threads")
+    for what, fn in (("plan", lambda: plan.forward(dQ, dK, dV, dO, masked=False)),
+                     ("drop-in, descending order",
+                      lambda: gpu.attention_fwd(dQ, dK, dV, dO, bsf, order, masked=False))):
+        check_whole_graph(f"cfg4 tile-dense {what}", run(fn), want)
 
 
 @pytest.mark.slow
 def test_config5_full_size(gpu):
+    """Config 5 at full size (121.9 M edges, 4 heads): the converter in full;
+    masked attention on every row for the compiled plan and the drop-in
+    launch in natural order; tile-dense (15.5 TFLOP of tile work for the CPU
+    oracle, minutes on 16 threads) on 608 sampled row ranges of 64 rows
+    (1.6 % of the rows) including the heaviest windows."""
     c = gpu.CONFIGS[5]
     t0 = time.time()
     rp, ci = c.graph()
@@ -732,27 +794,31 @@ def test_config5_full_size(gpu):
     dQ, dK, dV = (gpu.DeviceArray.from_numpy(x.view(np.uint16)) for x in (Q, K, V))
     dO = gpu.DeviceArray((n, H, 64), np.float32)
     hb = bsf.to_host()
-    ranges = sample_rows(hb, n, stride_rows=40000)
-    rows = np.unique(np.concatenate([np.arange(a, b) for a, b in ranges]))
-    # oracle inputs restricted to the rows needed (sampled rows + neighbours)
     Qf, Kf, Vf = (x.astype(np.float32) for x in (Q, K, V))
+    del Q, K, V
     plan = gpu.Plan(bsf, None, H=H)
     plan.compile()
-    for masked in (True, False):
+
+    def run(fn):
         dO.fill_bytes(0xFF)
-        plan.forward(dQ, dK, dV, dO, masked=masked)
+        fn()
         gpu.synchronize()
-        got = dO.numpy()
-        assert np.all(np.isfinite(got))
-        worst = (0.0, 0.0)
-        for (a, b) in ranges:
-            if masked:
-                want = orc.masked_attention(n, 64, H, Qf, Kf, Vf, rp, ci, 1.0, a, b)[a:b]
-            else:
-                want = orc.tile_dense_attention(n, 64, H, Qf, Kf, Vf, hb.window_offsets,
-                                                hb.block_col_indices, 1.0, a, b)[a:b]
-            mabs, mrel = errors(got[a:b], want)
-            assert mabs <= ABS_TOL and mrel <= REL_TOL, f"rows {a}:{b} masked={masked}: {mabs} {mrel}"
-            worst = (max(worst[0], mabs), max(worst[1], mrel))
-        log(f"cfg5 masked={masked}: {len(ranges)} row ranges ({len(rows)} rows) within tolerance, "
-            f"worst max_abs={worst[0]:.3e} max_rel={worst[1]:.3e}")
+        return dO.numpy()
+
+    th = oracle_threads()
+    t0 = time.time()
+    want = orc.masked_attention(n, 64, H, Qf, Kf, Vf, rp, ci, 1.0, threads=th)
+    log(f"cfg5 masked oracle, whole graph: {time.time()-t0:.2f}s on {th} threads")
+    for what, fn in (("compiled plan", lambda: plan.forward(dQ, dK, dV, dO, masked=True)),
+                     ("drop-in, natural order",
+                      lambda: gpu.attention_fwd(dQ, dK, dV, dO, bsf, None, masked=True, H=H))):
+        check_whole_graph(f"cfg5 masked {what}", run(fn), want)
+    del want
+    ranges = sample_rows(hb, n, stride_rows=4000)
+
+    def want_rows(a, b):
+        return orc.tile_dense_attention(n, 64, H, Qf, Kf, Vf, hb.window_offsets,
+                                        hb.block_col_indices, 1.0, a, b, threads=th)[a:b]
+
+    check_sampled("cfg5 tile-dense plan", run(lambda: plan.forward(dQ, dK, dV, dO, masked=False)),
+                  ranges, want_rows)
