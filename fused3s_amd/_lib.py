@@ -1,16 +1,18 @@
 """ctypes bindings of the two native libraries (include/f3s_capi.h,
 include/f3s_host.h).
 
-The libraries are loaded from this package directory only; if one is missing
-the import of the binding fails loudly (there is no Python or CPU fallback
-for any function of the path).
+The libraries are loaded from this package directory (or, for the CPU
+suite's sanitizer run, from the directory F3S_LIB_DIR names, which holds the
+instrumented build); if one is missing the import of the binding fails loudly
+(there is no Python or CPU fallback for any function of the path).
 """
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
-PKG = Path(__file__).resolve().parent
+PKG = Path(os.environ.get("F3S_LIB_DIR") or Path(__file__).resolve().parent)
 
 c_i32, c_i64, c_u64, c_f32, c_dbl = C.c_int32, C.c_int64, C.c_uint64, C.c_float, C.c_double
 c_vp = C.c_void_p

@@ -80,6 +80,30 @@ def build_host(verbose: bool = True) -> Path:
     return out
 
 
+SAN_DIR = OBJ / "san"
+SAN_FLAGS = ["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+             "-fno-sanitize-recover=undefined"]
+
+
+def build_host_sanitized(verbose: bool = True) -> Path:
+    """ASan + UBSan build of libf3s_host.so in fused3s_amd/_build/san/, beside
+    a link to the normal libf3s_hip.so (the HIP library is not instrumented),
+    for the CPU suite's sanitizer run (tests/sanitize.sh, which loads the
+    libraries from that directory through F3S_LIB_DIR)."""
+    SAN_DIR.mkdir(parents=True, exist_ok=True)
+    hip = SAN_DIR / "libf3s_hip.so"
+    if hip.is_symlink() or hip.exists():
+        hip.unlink()
+    hip.symlink_to(PKG / "libf3s_hip.so")
+    out = SAN_DIR / "libf3s_host.so"
+    flags = [f for f in HOST_FLAGS if f != "-O3"] + SAN_FLAGS
+    cmd = ["g++", *flags, "-shared", *(str(CSRC / s) for s in HOST_SOURCES),
+           "-L", str(SAN_DIR), "-lf3s_hip", "-Wl,-rpath,$ORIGIN", "-o", str(out)]
+    _run(cmd, verbose)
+    _run(["make", "-s", "-C", str(ROOT / "oracle"), "sanitize"], verbose)
+    return out
+
+
 def build_oracle(verbose: bool = True) -> None:
     _run(["make", "-s", "-C", str(ROOT / "oracle")], verbose)
 
@@ -125,4 +149,7 @@ def build_all(verbose: bool = True) -> None:
 
 
 if __name__ == "__main__":
-    build_all(verbose="-q" not in sys.argv)
+    if "--sanitize" in sys.argv:
+        build_host_sanitized(verbose="-q" not in sys.argv)
+    else:
+        build_all(verbose="-q" not in sys.argv)

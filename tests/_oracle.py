@@ -6,12 +6,14 @@ Test infrastructure: used only as the checker.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 import numpy as np
 
 ROOT = Path(__file__).resolve().parents[1]
-ORACLE_SO = ROOT / "oracle" / "liboracle.so"
+# F3S_ORACLE_LIB: the sanitizer run's instrumented build (tests/sanitize.sh)
+ORACLE_SO = Path(os.environ.get("F3S_ORACLE_LIB") or ROOT / "oracle" / "liboracle.so")
 REF_SO = ROOT / "oracle" / "_ref" / "libref_cpu_baseline.so"
 
 _vp, _i32, _i64, _f32 = C.c_void_p, C.c_int32, C.c_int64, C.c_float

@@ -125,12 +125,25 @@ def test_invalid_contents_are_rejected(tmp_path):
         f3s.load_graph(p)
 
 
-@pytest.mark.parametrize("k", [1, 50, 100000])
-def test_offsets_past_the_tile_count_are_rejected(tmp_path, k):
+def ascending_tail_graph():
+    """32 nodes, two windows: rows 0-15 link to nodes 0 and 16 (window 0
+    holds block columns 0 and 1, the last tiles of the list), rows 16-31
+    have no edges, so a walk past window 0's end reads ascending columns up
+    to the end of block_col and then past it."""
+    rp = np.zeros(33, np.int32)
+    rp[1:17] = 2 * np.arange(1, 17)
+    rp[17:] = 32
+    ci = np.tile(np.array([0, 16], np.int32), 16)
+    return rp, ci
+
+
+@pytest.mark.parametrize("graph,k", [("random", 1), ("random", 50), ("random", 100000),
+                                     ("tail", 1), ("tail", 7)])
+def test_offsets_past_the_tile_count_are_rejected(tmp_path, graph, k):
     # window_offsets = [0, T + k, ..., T]: an entry past T must be rejected
     # before any block column is read through it (the block_col array holds
     # exactly T entries), with a valid checksum in front of it.
-    rp, ci = random_csr(64, 4, 7)
+    rp, ci = random_csr(64, 4, 7) if graph == "random" else ascending_tail_graph()
     bsf = oracle_bsf(rp, ci)
     T = int(bsf.window_offsets[-1])
     wo = bsf.window_offsets.copy()
