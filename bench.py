@@ -81,6 +81,49 @@ def compulsory_bytes(n: int, H: int, W: int, T: int, kv_rows: int, masked: bool,
     return int(b)
 
 
+LOCALITY_ORDERS = ("sorted-xcd", "lowest-block-column", "top-hub", "random")
+
+
+def locality_order(kind: str, rp, ci, offs, bcol) -> np.ndarray:
+    """A window order for the locality experiments: descending workload,
+    windows by their lowest block column, windows grouped by their attended
+    column of highest degree, or random; all but random laid out so that each
+    eighth of the sequence runs on one XCD (given an order, workgroup b of 4
+    windows runs on XCD b mod 8)."""
+    cnt = np.diff(offs)
+    W = len(cnt)
+    if kind == "random":
+        return np.random.default_rng(1).permutation(W).astype(np.int32)
+    if kind == "sorted-xcd":
+        seq = np.argsort(-cnt, kind="stable")
+    elif kind == "lowest-block-column":
+        first = np.where(cnt > 0, bcol[np.minimum(offs[:-1], max(len(bcol) - 1, 0))], 1 << 30)
+        seq = np.argsort(first, kind="stable")
+    else:
+        n = len(rp) - 1
+        deg = np.diff(rp)
+        rows = np.repeat(np.arange(n), deg)
+        top = np.full(W, -1, np.int64)
+        best = np.full(W, -1, np.int64)
+        # per window, the attended column of highest degree (ties: lowest id)
+        key = deg[ci].astype(np.int64) * (n + 1) + (n - ci)
+        np.maximum.at(best, rows // 16, key)
+        has = best >= 0
+        top[has] = n - best[has] % (n + 1)
+        seq = np.lexsort((-cnt, top))
+    # XCD x owns the positions of workgroups b = x, x + 8, ...; it takes the
+    # x-th contiguous part of the sequence, in order (every window once)
+    pos = np.arange(W)
+    xcd = (pos // 4) % 8
+    out = np.empty(W, np.int32)
+    start = 0
+    for x in range(8):
+        p = pos[xcd == x]
+        out[p] = seq[start:start + len(p)]
+        start += len(p)
+    return out
+
+
 def read_profile(path: Path, key: str) -> float | None:
     """`key value` line of a committed rocprofv3 summary."""
     if not path.exists():
@@ -187,9 +230,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=4)
     ap.add_argument("--semantics", choices=["masked", "tile_dense"], default="masked")
-    ap.add_argument("--order", choices=["auto", "sorted", "natural"], default="auto",
+    ap.add_argument("--order", choices=["auto", "sorted", "natural"] + list(LOCALITY_ORDERS),
+                    default="auto",
                     help="window order: descending workload (the reference's sort) or natural; "
-                         "auto = natural for the community-ordered SBM config, else sorted")
+                         "auto = natural for the community-ordered SBM config, else sorted; "
+                         "the others are locality experiments, laid out so that each eighth "
+                         "of the sequence runs on one XCD")
     ap.add_argument("--seg", type=int, default=0,
                     help="plan segment size in tiles (0 = automatic)")
     ap.add_argument("--no-compile", action="store_true",
@@ -273,6 +319,11 @@ def main() -> int:
     conv_ms = convert_phases_ms(csr, bsf, stream)
     use_sorted = args.order == "sorted" or (args.order == "auto" and c.kind != "sbm")
     order = f3s.window_order_device(bsf, stream) if use_sorted else None
+    if args.order in LOCALITY_ORDERS:
+        hb = bsf.to_host()
+        order = f3s.DeviceArray.from_numpy(
+            locality_order(args.order, rp, ci, hb.window_offsets, hb.block_col_indices), stream)
+        del hb
     plan = None
     plan_ms = None
     compiled = masked and not args.no_compile and not args.unplanned
@@ -377,7 +428,8 @@ def main() -> int:
         "data": "synthetic (seeded generator; no dataset download)",
         "config": {"workload": f"cfg{c.cfg}: {c.name}" + (f" with H={H}" if args.heads else ""), "nodes": n, "edges": nnz, "heads": H,
                    "head_dim": d, "semantics": args.semantics,
-                   "window_order": "descending workload" if use_sorted else "natural",
+                   "window_order": ("descending workload" if use_sorted else
+                                    args.order if args.order in LOCALITY_ORDERS else "natural"),
                    "launch": "f3s_attention_fwd (unplanned)" if args.unplanned else "plan",
                    "row_windows": bsf.W,
                    "active_tiles": bsf.T, "attended_tile_columns": occ_sum},

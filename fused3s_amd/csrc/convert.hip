@@ -401,7 +401,9 @@ convert_hubs(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ co
              const int32_t* __restrict__ num_hubs, int32_t* __restrict__ err)
 {
     __shared__ ConvLds<FILL, NT> L;
-    const int32_t nh = hubs ? *num_hubs : W;
+    // convert_light lists each window at most once (num_hubs <= W); the clamp
+    // keeps the list read inside its W + 1 entries whatever the count holds
+    const int32_t nh = hubs ? min(*num_hubs, W) : W;
     for (int32_t i = blockIdx.x; i < nh; i += gridDim.x) {
         const int32_t w = hubs ? hubs[i] : i;
         if (w < 0 || w >= W) continue;   // uniform
