@@ -180,11 +180,11 @@ fused_attention_kernel(const AttnParams p)
         const int64_t cb = p.chunk_base[item_idx], ce = p.chunk_base[item_idx + 1];
         const uint32_t piece_off = head_off + 16 * (lane & 7);
         uint32_t* meta = reinterpret_cast<uint32_t*>(L.off);   // 4 records of this wave
-        const uint4* __restrict__ rec = reinterpret_cast<const uint4*>(p.columns);
-        uint4 blk = cb < ce ? rec[cb * 16 + lane] : make_uint4(0u, 0u, 0u, 0u);
+        const u4* __restrict__ rec = reinterpret_cast<const u4*>(p.columns);
+        u4 blk = cb < ce ? rec[cb * 16 + lane] : u4{0u, 0u, 0u, 0u};
         for (int64_t c0 = cb; c0 < ce; c0 += 4) {
             F3S_WAVE_LDS_SYNC();   // the previous block's reads of meta are done
-            *reinterpret_cast<uint4*>(&meta[4 * lane]) = blk;
+            *reinterpret_cast<u4*>(&meta[4 * lane]) = blk;
             F3S_WAVE_LDS_SYNC();
             if (c0 + 4 < ce) blk = rec[(c0 + 4) * 16 + lane];   // next block, in flight
             const int nk = (int)min((int64_t)4, ce - c0);
@@ -364,14 +364,24 @@ fused_attention_kernel(const AttnParams p)
     lrow += __shfl_xor(lrow, 32, kWave);
     if (slot < 0) {
         const float inv = lrow > 0.f ? 1.0f / lrow : 0.f;
-        if (orow < n) {
-            float* op = p.O + ((int64_t)orow * H + h) * kD + 16 * g;
+        // O leaves in whole rows: the lane's 16 values (row r, dims
+        // 16g..16g+15) pass through this wave's LDS stage so that each store
+        // instruction writes four complete 256-byte rows instead of 16-byte
+        // pieces of all sixteen.
+        F3S_WAVE_LDS_SYNC();   // this wave's last reads of its stage are done
+        float* ost = reinterpret_cast<float*>(L.stage);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                float4 o4 = make_float4(st.acc[0][v] * inv, st.acc[1][v] * inv, st.acc[2][v] * inv,
-                                        st.acc[3][v] * inv);
-                *reinterpret_cast<float4*>(op + 4 * v) = o4;
-            }
+        for (int v = 0; v < 4; ++v)
+            *reinterpret_cast<f4*>(&ost[r * kOutStride + 16 * g + 4 * v]) =
+                f4{st.acc[0][v] * inv, st.acc[1][v] * inv, st.acc[2][v] * inv, st.acc[3][v] * inv};
+        F3S_WAVE_LDS_SYNC();
+        const int c4 = 4 * (lane & 15);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int rr = 4 * v + (lane >> 4);
+            const f4 o4 = *reinterpret_cast<const f4*>(&ost[rr * kOutStride + c4]);
+            const int32_t row = w * 16 + rr;
+            if (row < n) store_out(p.O + ((int64_t)row * H + h) * kD + c4, o4);
         }
         return;
     }

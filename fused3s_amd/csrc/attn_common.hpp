@@ -14,6 +14,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 64;             // feature dim per head (FEAT_DIM_FIXED, fused3s_v2.cu:41)
 constexpr int kRowBytes = kD * 2;  // one fp16 K/V/Q row of one head
@@ -40,11 +41,24 @@ struct SplitInfo {
 // 16 consecutive rows then hit 64 distinct LDS banks.
 constexpr int kStageRow = kD + 8;   // halves
 
+// The epilogue stages O (16 rows of 64 floats) through a wave's stage, rows
+// 68 floats apart so the 16 rows start in different LDS banks.
+constexpr int kOutStride = kD + 4;   // floats
+// O stores of the epilogue: whole rows (four per instruction, see
+// fused_attention_kernel), non-temporal -- O is written once and never read
+// by the pass, so its lines should not displace the K/V rows in the caches.
+__device__ __forceinline__ void store_out(float* dst, f4 v)
+{
+    __builtin_nontemporal_store(v, reinterpret_cast<f4*>(dst));
+}
+
 struct __align__(16) WaveLds {
     uint32_t off[kRing];   // byte offset of the slot's K/V row for this wave's head
     uint32_t rm[kRing];    // rows of the window that attend the slot
-    _Float16 stage[kChunk * kStageRow];   // the chunk's K rows, then its V rows
+    _Float16 stage[kChunk * kStageRow];   // the chunk's K rows, then its V rows; O at the end
 };
+static_assert(sizeof(_Float16) * kChunk * kStageRow >= sizeof(float) * 16 * kOutStride,
+              "the stage holds a window's O rows");
 
 struct AttnParams {
     const _Float16* Q;
@@ -166,7 +180,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 __device__ __forceinline__ h8 load_h8(__amdgpu_buffer_rsrc_t rs, uint32_t off)
 {
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
     u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
     return __builtin_bit_cast(h8, v);
 }
