@@ -80,3 +80,39 @@ def test_noalloc_rejects_graphs_past_its_scratch(gpu):
     st = lib.f3s_attention_fwd_noalloc(dummy, dummy, dummy, dummy, dummy, dummy, None, None,
                                        W, 16 * W, 64, 1, 1.0, None)
     assert st == 5 and b"4194304" in lib.f3s_last_error()
+
+
+def test_noalloc_replays_from_a_hip_graph(gpu):
+    # The allocation-free launch captured into a graph (no allocation, no
+    # host synchronisation and no memset in it) and replayed three times,
+    # with eager library work and synchronisations between the replays:
+    # every replay must reproduce the eager result bit for bit.
+    torch = pytest.importorskip("torch")
+    from fused3s_amd import _lib
+    lib = _lib.hip()
+    rp, ci = hub_graph(40000, 83, {11: 30000, 20000: 1000, 30001: 25000})
+    p = Problem(gpu, rp, ci, H=2, normal=True, seed=83)
+    bsf = p.bsf
+    other = gpu.DeviceArray(p.dO.shape, np.float32)
+    for masked in (True, False):
+        args = (p.dQ.ptr, p.dK.ptr, p.dV.ptr, p.dO.ptr, bsf.window_offsets.ptr, bsf.block_col.ptr,
+                bsf.tile_mask.ptr if masked else None, None, bsf.W, bsf.n, 64, p.H, 0.125)
+        want = call(lib.f3s_attention_fwd, p, masked)       # eager, allocating entry point
+        st = lib.f3s_attention_fwd_noalloc(*args, None)     # eager warm-up of the variant
+        assert st == 0
+        gpu.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            st = lib.f3s_attention_fwd_noalloc(*args, torch.cuda.current_stream().cuda_stream)
+        assert st == 0, lib.f3s_last_error()
+        for rep in range(3):
+            p.dO.fill_bytes(0xFF)
+            # eager work between replays: the same pass into another buffer
+            assert lib.f3s_attention_fwd(*args[:3], other.ptr, *args[4:], None) == 0
+            gpu.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = p.dO.numpy()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (masked, rep)
+            assert np.array_equal(other.numpy().view(np.uint32), want.view(np.uint32))
+        del g
