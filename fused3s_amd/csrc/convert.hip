@@ -843,6 +843,85 @@ convert_light(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ c
     if (tid == 0 && *L.bad) atomicOr(err, kErrCol);
 }
 
+// Hub windows heaviest first.  convert_light lists them in the order its
+// workgroups find them; rank_hubs writes the list again, ordered by
+// descending edge count (ties: ascending window index, so the order is
+// deterministic), and the hub launch that follows gives each listed window a
+// workgroup of its own, dispatched in list order, so the longest windows
+// start first.  Every workgroup of rank_hubs loads the keys of the whole list
+// (up to kHubSortCap) into LDS and places 64 of them at their ranks, four
+// lanes per entry each counting the smaller keys in a quarter of the list;
+// keys are unique, so the ranks are a permutation.  A longer list is copied
+// as listed.
+constexpr int kHubSortCap = 4096;
+constexpr int kHubLaunch = 2048;   // hub-launch workgroups (one per listed window up to this)
+
+__global__ void __launch_bounds__(256)
+rank_hubs(const int32_t* __restrict__ row_ptr, int32_t n, int32_t W,
+          const int32_t* __restrict__ hubs, const int32_t* __restrict__ num_hubs,
+          int32_t* __restrict__ sorted)
+{
+    __shared__ __align__(16) uint64_t key[kHubSortCap];
+    const int32_t nh = min(*num_hubs, W);
+    const int tid = threadIdx.x;
+    if (nh > kHubSortCap) {   // uniform: copy in listing order
+        for (int64_t i = (int64_t)blockIdx.x * 256 + tid; i < nh; i += (int64_t)gridDim.x * 256)
+            sorted[i] = hubs[i];
+        return;
+    }
+    const int32_t base = blockIdx.x * 64;
+    if (base >= nh) return;   // uniform
+    // The thread's list entries, then their row pointers: two rounds of loads
+    // in flight instead of one dependent pair per entry.
+    constexpr int kPer = kHubSortCap / 256;
+    int32_t wv[kPer], lo[kPer], hi[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = tid + 256 * k;
+        wv[k] = i < nh ? hubs[i] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const bool ok = (uint32_t)wv[k] < (uint32_t)W;
+        lo[k] = ok ? row_ptr[wv[k] * 16] : 0;
+        hi[k] = ok ? row_ptr[min(n, wv[k] * 16 + 16)] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        // (~edges, window) ascending = edges descending, window ascending; an
+        // entry naming no window sorts last, keyed by its position
+        const int i = tid + 256 * k;
+        if (i >= nh) break;
+        uint64_t key_i = (0xffffffffull << 32) | (uint32_t)i;
+        if ((uint32_t)wv[k] < (uint32_t)W) {
+            const uint32_t edges = (uint32_t)min(max(1, hi[k] - lo[k]), 0x7fffffff);
+            key_i = ((uint64_t)(~edges) << 32) | (uint32_t)wv[k];
+        }
+        key[i] = key_i;
+    }
+    __syncthreads();
+    // lanes 4e..4e+3 of a wave rank entry base + tid / 4, each over a quarter
+    // of the list in steps of eight keys (four 16-byte LDS reads, from a
+    // multiple of 8); their counts add up with two lane swaps
+    const int32_t i = base + tid / 4;
+    const uint64_t ki = key[i < nh ? i : 0];
+    const int32_t quarter = ((nh + 31) / 32) * 8;   // a multiple of 8
+    const int32_t j0 = min(nh, (tid & 3) * quarter), j1 = min(nh, j0 + quarter);
+    int32_t rank = 0;
+    int32_t j = j0;
+    for (; j + 8 <= j1; j += 8) {
+        const ulonglong2* k2 = reinterpret_cast<const ulonglong2*>(&key[j]);
+        const ulonglong2 a = k2[0], b = k2[1], c = k2[2], d = k2[3];
+        rank += (a.x < ki) + (a.y < ki) + (b.x < ki) + (b.y < ki) + (c.x < ki) + (c.y < ki) +
+                (d.x < ki) + (d.y < ki);
+    }
+    for (; j < j1; ++j) rank += key[j] < ki ? 1 : 0;
+    rank += __shfl_xor(rank, 1, kWave);
+    rank += __shfl_xor(rank, 2, kWave);
+    if (i < nh && (tid & 3) == 0)
+        sorted[rank] = (ki >> 32) == 0xffffffffull ? -1 : (int32_t)(uint32_t)ki;
+}
+
 // int64 window offsets -> the caller's int32 offsets; thread 0 also reports
 // the error bits and the tile count for the host (status[0], status[1]).
 __global__ void offsets_to_i32(const int64_t* __restrict__ in, int32_t* __restrict__ out,
@@ -867,14 +946,16 @@ __global__ void fill_status(const int32_t* __restrict__ window_offsets, int32_t 
     }
 }
 
-// Per-call workspace of the converter, one pool allocation: status words
-// (error bits, hub count, two int64 results), the hub window list and, for
-// the count pass, the counts, their int64 scan and its temporaries.
+// Per-call workspace of the converter, one allocation: status words (error
+// bits, hub count, two int64 results), the hub window list as found and as
+// ordered heaviest first and, for the count pass, the counts, their int64
+// scan and its temporaries.
 struct ConvertScratch {
     int32_t* err;
     int32_t* num_hubs;
     int64_t* status;
     int32_t* hubs;
+    int32_t* hubs_sorted;
     int32_t* counts;
     int64_t* offs64;
     int64_t* tmp;
@@ -888,13 +969,15 @@ static f3s_status convert_scratch(StreamBuffer& buf, int32_t W, bool count, Conv
     const size_t offs = count ? sizeof(int64_t) * ((size_t)W + 1) : 0;
     const size_t tmp = count ? sizeof(int64_t) * (size_t)scan_tmp_elems(W) : 0;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    F3S_TRY(buf.reserve(al(head) + al(hubs) + al(counts) + al(offs) + al(tmp)));
+    F3S_TRY(buf.reserve(al(head) + 2 * al(hubs) + al(counts) + al(offs) + al(tmp)));
     char* p = static_cast<char*>(buf.ptr);
     s.err = reinterpret_cast<int32_t*>(p);
     s.num_hubs = s.err + 1;
     s.status = reinterpret_cast<int64_t*>(p + 16);
     p += al(head);
     s.hubs = reinterpret_cast<int32_t*>(p);
+    p += al(hubs);
+    s.hubs_sorted = reinterpret_cast<int32_t*>(p);
     p += al(hubs);
     s.counts = reinterpret_cast<int32_t*>(p);
     p += al(counts);
@@ -913,8 +996,8 @@ template <bool FILL>
 static f3s_status launch_pass(const int32_t* row_ptr, const int32_t* col_idx, int32_t n,
                               int64_t nnz, int32_t W, int32_t* counts,
                               const int32_t* window_offsets, int32_t* block_col,
-                              uint16_t* tile_mask, int32_t* hubs, int32_t* num_hubs,
-                              int32_t* err, hipStream_t stream)
+                              uint16_t* tile_mask, int32_t* hubs, int32_t* hubs_sorted,
+                              int32_t* num_hubs, int32_t* err, hipStream_t stream)
 {
     if (W <= 0) return F3S_OK;
     if ((int64_t)W > 32LL * kLightMaxWords) {
@@ -936,10 +1019,13 @@ static f3s_status launch_pass(const int32_t* row_ptr, const int32_t* col_idx, in
                        row_ptr, col_idx, n, nnz, W, counts, window_offsets, block_col,
                        tile_mask, hubs, num_hubs, err);
     F3S_HIP(hipGetLastError());
-    const int64_t hub_grid = 2 * (int64_t)(cus > 0 ? cus : 1);
+    const int32_t rank_wgs = (int32_t)ceil_div(W < kHubSortCap ? W : kHubSortCap, 64);
+    hipLaunchKernelGGL(rank_hubs, dim3((unsigned)rank_wgs), dim3(256), 0, stream, row_ptr, n, W,
+                       hubs, num_hubs, hubs_sorted);
+    const int64_t hub_grid = kHubLaunch;
     hipLaunchKernelGGL((convert_hubs<FILL, kHubThreads>), dim3((unsigned)(W < hub_grid ? W : hub_grid)),
                        dim3(kHubThreads), 0, stream, row_ptr, col_idx, n, nnz, W, counts,
-                       window_offsets, block_col, tile_mask, hubs, num_hubs, err);
+                       window_offsets, block_col, tile_mask, hubs_sorted, num_hubs, err);
     F3S_HIP(hipGetLastError());
     return F3S_OK;
 }
@@ -959,13 +1045,14 @@ static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, i
     F3S_HIP(hipMemsetAsync(s.err, 0, 2 * sizeof(int32_t), stream));
     if (count) {
         F3S_TRY(launch_pass<false>(row_ptr, col_idx, n, nnz, W, s.counts, nullptr, nullptr,
-                                   nullptr, s.hubs, s.num_hubs, s.err, stream));
+                                   nullptr, s.hubs, s.hubs_sorted, s.num_hubs, s.err, stream));
         F3S_TRY(exclusive_scan_i32_to_i64(s.counts, s.offs64, W, s.tmp, stream));
         hipLaunchKernelGGL(offsets_to_i32, dim3((unsigned)ceil_div(W + 1, 256)), dim3(256), 0,
                            stream, s.offs64, window_offsets, (int64_t)W + 1, s.err, s.status);
     } else {
         F3S_TRY(launch_pass<true>(row_ptr, col_idx, n, nnz, W, nullptr, window_offsets,
-                                  block_col, tile_mask, s.hubs, s.num_hubs, s.err, stream));
+                                  block_col, tile_mask, s.hubs, s.hubs_sorted, s.num_hubs, s.err,
+                                  stream));
         hipLaunchKernelGGL(fill_status, dim3(1), dim3(64), 0, stream, window_offsets, W, s.err,
                            s.status);
     }
