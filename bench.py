@@ -173,6 +173,27 @@ def time_passes(f3s, one_pass, stream, reps: int) -> np.ndarray:
     return np.array([a.elapsed_ms(b) for a, b in evs])
 
 
+def gather_ceiling(f3s, dK, dV, rows: int, H: int, count: int, stream, reps: int = 10,
+                   seed: int = 11) -> dict:
+    """The device's random-gather ceiling for the pass's load shape
+    (f3s_probe_gather): `count` columns (rounded down to 32) of uniformly
+    random rows < `rows`, the K and V row of head 0 of each, on the
+    workload's own tensors; mean of `reps` launches timed with events on
+    `stream`."""
+    count = max(32, count // 32 * 32)
+    idx = np.random.default_rng(seed).integers(0, rows, count, dtype=np.int64).astype(np.int32)
+    didx = f3s.DeviceArray.from_numpy(idx, stream)
+    cpw = 8
+    out = f3s.DeviceArray(((count // 32 + cpw - 1) // cpw,), np.uint32)
+    stride = H * 128
+    t = time_passes(f3s, lambda: f3s.probe_gather(dK, dV, rows, stride, didx, out, cpw, stream),
+                    stream, reps)
+    mean = float(t.mean())
+    return {"rows_per_s": 2 * count / (mean * 1e-3), "GBps": 2 * count * 128 / (mean * 1e-3) / 1e9,
+            "probe_us": mean * 1e3, "columns": count, "table_rows": rows,
+            "table_bytes_each": rows * stride}
+
+
 def cpu_baseline(rp, ci, Q, K, V, n: int, d: int) -> dict | None:
     """The reference's cpu_sparse_attention_csr (single thread) over the
     whole graph, on this host."""
@@ -251,6 +272,9 @@ def main() -> int:
                     help="skip timing the reference's semantics and launch shape after the "
                          "timed region")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gather-probe", action="store_true",
+                    help="only measure the random-gather ceiling (f3s_probe_gather) over "
+                         "tables of several sizes and exit")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run device-to-device copies of this size (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes) and exit")
@@ -283,6 +307,19 @@ def main() -> int:
         # read + write bytes over the fastest copy: the practical HBM rate
         print(json.dumps({"copy_probe_bytes": nb, "launches": args.steps,
                           "copy_ms": times, "copy_GBps_rw": 2 * nb / best / 1e6}), flush=True)
+        return 0
+    if args.gather_probe:
+        # uniformly random 128-byte K and V rows, the config-4 pass's column
+        # count, tables from L2-resident (1 MB each) to past the Infinity
+        # Cache (512 MB each)
+        f3s.init()
+        stream = f3s.Stream()
+        for rows in (8192, 1_000_000, 4_000_000):
+            tk = f3s.DeviceArray((rows, 64), np.uint16, zero=True)
+            tv = f3s.DeviceArray((rows, 64), np.uint16, zero=True)
+            r = gather_ceiling(f3s, tk, tv, rows, 1, 16_907_486, stream, reps=max(3, args.steps))
+            print(json.dumps({"gather_probe": r}), flush=True)
+            del tk, tv
         return 0
     f3s.init()
     c = f3s.CONFIGS[args.config]
@@ -468,6 +505,17 @@ def main() -> int:
         "plan_compiled": compiled,
         "device": f3s.device_name(),
     }
+
+    # the device's random-gather ceiling for this workload's tensors and column
+    # count, beside the rate at which the pass gathers rows
+    rows_pass = 2 * H * (occ_sum if masked else bsf.T * 16)
+    gc = gather_ceiling(f3s, dK, dV, n, H, occ_sum, stream)
+    gc["pass_rows_per_s"] = rows_pass / (kavg * 1e-3)
+    gc["pass_over_ceiling"] = gc["pass_rows_per_s"] / gc["rows_per_s"]
+    gc["note"] = ("f3s_probe_gather: uniformly random K and V rows of 128 B (head 0), the pass's "
+                  "load shape, on the workload's tensors; the pass's rows are its gathered K and "
+                  "V rows per head (masked: attended columns; tile-dense: 16 per tile)")
+    res["gather_ceiling"] = gc
 
     if not args.no_reference_launches:
         # The reference's own semantics (tile-dense, src/fused3s_v2.cu:145-228)

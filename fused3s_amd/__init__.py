@@ -13,7 +13,7 @@ from .graph import (BlockSparseFormat, DeviceBSF, DeviceCSR, GraphData, bsf_stat
                     convert_csr_to_block_sparse, convert_device, generate_balanced_window_order,
                     load_csr_graph, load_graph, save_graph, window_order_device)
 from .attention import (Plan, attention_fwd, attention_fwd_timed, cast_f32_to_f16,
-                        naive_attention_fwd)
+                        naive_attention_fwd, probe_gather)
 from .configs import CONFIGS, Config
 
 __all__ = [
@@ -23,5 +23,6 @@ __all__ = [
     "convert_csr_to_block_sparse", "convert_device", "generate_balanced_window_order",
     "load_csr_graph", "load_graph", "save_graph", "window_order_device", "Plan",
     "attention_fwd", "attention_fwd_timed", "cast_f32_to_f16", "naive_attention_fwd",
+    "probe_gather",
     "CONFIGS", "Config",
 ]

@@ -64,6 +64,7 @@ HIP_API = {
     "f3s_plan_stats": (c_i32, [c_vp, P_i64, P_i64, P_i64, P_i64, P_i64]),
     "f3s_attention_fwd_planned": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                           c_i32, c_i32, c_i32, c_f32, c_vp]),
+    "f3s_probe_gather": (c_i32, [c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_vp, c_vp]),
 }
 
 # name -> (restype, argtypes) for libf3s_host.so

@@ -120,3 +120,15 @@ def naive_attention_fwd(Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: Devic
                                              csr.col_idx.ptr, csr.n, d, scale,
                                              stream.handle if stream else None),
           "f3s_naive_attention_fwd")
+
+
+def probe_gather(K: DeviceArray, V: DeviceArray, rows: int, row_stride: int,
+                 idx: DeviceArray, out: DeviceArray, cpw: int = 8,
+                 stream: Stream | None = None) -> None:
+    """f3s_probe_gather (measurement only): loads the 128-byte K and V rows
+    named by the int32 ``idx`` (a multiple of 32 entries) in the fused pass's
+    load shape and folds them into ``out`` (one uint32 per wave)."""
+    count = int(np.prod(idx.shape))
+    check(_lib.hip().f3s_probe_gather(K.ptr, V.ptr, rows, row_stride, idx.ptr, count, cpw,
+                                      out.ptr, stream.handle if stream else None),
+          "f3s_probe_gather")

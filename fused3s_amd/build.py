@@ -23,7 +23,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
-HIP_SOURCES = ["runtime.hip", "convert.hip", "attention.hip", "bsf_util.hip", "naive.hip"]
+HIP_SOURCES = ["runtime.hip", "convert.hip", "attention.hip", "bsf_util.hip", "naive.hip",
+               "probe.hip"]
 HOST_SOURCES = ["host/gen.cpp", "host/graph.cpp", "host/graph_file.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -359,7 +359,6 @@ fused_attention_kernel(const AttnParams p)
     }
 
     // ---- epilogue ----
-    const int32_t orow = w * 16 + r;
     float lrow = st.l + __shfl_xor(st.l, 16, kWave);
     lrow += __shfl_xor(lrow, 32, kWave);
     if (slot < 0) {

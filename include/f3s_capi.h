@@ -226,6 +226,18 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q,
                                      int32_t n, int32_t d, int32_t H, float scale,
                                      void* stream);
 
+/* Measurement only (no reference counterpart): the device's random-gather
+ * ceiling for the fused pass's access pattern.  For each of `count` columns
+ * (a multiple of 32) it loads the 128-byte row at byte offset
+ * d_idx[i] * row_stride of K and of V (eight lanes x 16 bytes per row, 32
+ * columns per step, `cpw` steps per wave: the fused pass's load shape) and
+ * folds the bytes into d_out, one word per wave: ceil(count / 32 / cpw)
+ * words.  Tables hold `rows` rows (rows * row_stride <= 0xffff0000 bytes);
+ * a row past the table reads zero.  Asynchronous on `stream`. */
+f3s_status f3s_probe_gather(const uint16_t* K, const uint16_t* V, int64_t rows,
+                            int32_t row_stride, const int32_t* d_idx, int64_t count,
+                            int32_t cpw, uint32_t* d_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
