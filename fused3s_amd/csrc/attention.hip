@@ -91,7 +91,8 @@ fused_attention_kernel(const AttnParams p)
     int64_t item_idx;
     int h;
     if constexpr (TEAM == 1) {
-        const uint32_t gw = (uint32_t)(logical_block(p.xcd_contiguous) * WPG + wave);
+        const uint32_t gw =
+            (uint32_t)(logical_block(p.xcd_contiguous, p.prefix_blocks) * WPG + wave);
         item_idx = (int64_t)(gw / (uint32_t)H);
         h = (int)(gw % (uint32_t)H);
     } else {
@@ -119,15 +120,23 @@ fused_attention_kernel(const AttnParams p)
         }
     } else {
         const int64_t wi = item_idx / TEAM;
-        w = p.window_order ? p.window_order[wi] : (int32_t)wi;
+        if (p.heavy_mode == 3) {
+            // natural order: the listed medium windows first, then every
+            // window not listed (the team launch took the large ones)
+            if (wi < p.prefix_items) {
+                w = p.prefix_list[wi];
+            } else {
+                w = (int32_t)(wi - p.prefix_items);
+                if (w < p.W && ((p.heavy_listed[w >> 5] >> (w & 31)) & 1u)) return;
+            }
+        } else {
+            w = p.window_order ? p.window_order[wi] : (int32_t)wi;
+        }
         if (w < 0 || w >= p.W) return;
         const int32_t T = p.window_offsets[p.W];
         tb = max(0, min(p.window_offsets[w], T));
         te = max(tb, min(p.window_offsets[w + 1], T));
-        if (p.heavy_mode == 3) {
-            // natural order: the listed heavy windows belong to the team launch
-            if ((p.heavy_listed[w >> 5] >> (w & 31)) & 1u) return;
-        } else if (p.heavy_mode) {
+        if (p.heavy_mode == 1 || p.heavy_mode == 2) {
             // the heavy windows among the first heavy_max order positions
             // belong to the team launch (mode 2), all others to the one-wave
             // launch (mode 1); uniform over a team's workgroup
@@ -772,12 +781,16 @@ static void launch_mw(const AttnParams& p, int64_t waves, hipStream_t st)
         }
     }
     // Small launches use one-wave workgroups so they spread over all CUs.
+    // Prefix items fill whole workgroups: prefix_items * H is a multiple of 32.
+    AttnParams q = p;
     if (waves < 4 * 256 * 2) {
+        q.prefix_blocks = q.prefix_items * q.H;
         hipLaunchKernelGGL((fused_attention_kernel<MODE, 1, WIDE, 1>), dim3((unsigned)waves),
-                           dim3(kWave), 0, st, p);
+                           dim3(kWave), 0, st, q);
     } else {
+        q.prefix_blocks = q.prefix_items * q.H / 4;
         hipLaunchKernelGGL((fused_attention_kernel<MODE, 4, WIDE, 1>),
-                           dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
+                           dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, q);
     }
     if (p.num_split > 0)
         hipLaunchKernelGGL(merge_partials_kernel,
@@ -795,10 +808,11 @@ static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
 
 // Natural-order unplanned launches: the heavy windows of a class (more tiles
 // than the class threshold and, for the medium class, no more than the large
-// threshold), the first `cap` of them by index (deterministic), as a window
-// order for a team launch (entries past the count stay -1, which that launch
-// skips) and as bits of a bitmap the one-wave launch skips.  Blocks of 256
-// windows cover whole bitmap words.
+// threshold), the first `cap` of them by index (deterministic), as a list
+// (entries past the count stay -1, which the launches skip) -- the large
+// class for the team launch, the medium class for the one-wave launch to
+// start first -- and as bits of a bitmap the rest of the one-wave launch
+// skips.  Blocks of 256 windows cover whole bitmap words.
 struct HeavyClass {
     int32_t lo_min, lo_factor;   // in the class: more tiles than max(lo_min, lo_factor x mean)
     int32_t hi_min, hi_factor;   // ... and, if hi_min > 0, no more than max(hi_min, hi_factor x mean)
@@ -911,6 +925,37 @@ heavy_list(const int32_t* __restrict__ window_offsets, int32_t W, HeavyClass a, 
     if (lane == 1 && word + 1 < ((int64_t)W + 31) / 32) listed[word + 1] = (uint32_t)(tb >> 32);
 }
 
+// heavy_sort (one workgroup): the team launch's list heaviest first (ties by
+// index; empty entries last), so the dispatcher starts the longest windows
+// first, as the reference's descending order does.
+static_assert(kHeavyMaxWindows == 512, "heavy_sort sorts 512 entries, one per thread");
+__global__ void __launch_bounds__(512)
+heavy_sort(const int32_t* __restrict__ window_offsets, int32_t W, int32_t* __restrict__ list)
+{
+    __shared__ uint64_t key[kHeavyMaxWindows];
+    const int t = threadIdx.x;
+    const int32_t w = list[t];
+    const int32_t tiles = (w >= 0 && w < W) ? window_tiles(window_offsets, W, w) : -1;
+    key[t] = tiles >= 0 ? ((uint64_t)(uint32_t)(0x7fffffff - tiles) << 32) | (uint32_t)w
+                        : ~0ull;
+    __syncthreads();
+    for (int size = 2; size <= kHeavyMaxWindows; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const int u = t ^ stride;
+            if (u > t) {
+                const uint64_t a = key[t], b = key[u];
+                if ((a > b) == ((t & size) == 0)) {
+                    key[t] = b;
+                    key[u] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    const uint64_t k = key[t];
+    list[t] = k == ~0ull ? -1 : (int32_t)(uint32_t)k;
+}
+
 static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
 {
     if (p.num_items <= 0) return F3S_OK;
@@ -980,10 +1025,13 @@ static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const
     hipStream_t st = as_stream(stream);
     if (p.team == 1 && !d_window_order && !wide_features(n, H) && W > kHeavyMaxWindows) {
         // Natural order: the hubs can be anywhere.  Two small kernels list the
-        // large windows (the ordered rule) for teams of 16 and the medium ones
-        // for teams of 4 (a 16-wave team holds a CU's LDS, 4 waves a quarter
-        // of it), in a few tens of KB of scratch; one wave each takes the
-        // rest, skipping the listed windows.
+        // large windows (the ordered rule) and the medium ones, in a few tens
+        // of KB of scratch, and a third sorts the large ones heaviest first
+        // for a launch of 16-wave teams; the one-wave launch then starts the
+        // medium windows (dealt round-robin to the XCDs) before all others,
+        // which follow in natural order, XCD-contiguous, skipping the listed
+        // windows.  (Teams of 4 for the medium windows measured slower: their
+        // launch cannot start before the large teams' ends.)
         const HeavyClass large{kHeavyMinTiles, kHeavyMeanFactor, 0, 0, kHeavyMaxWindows};
         const HeavyClass medium{kHeavyMinTilesNat, kHeavyMeanFactorNat, kHeavyMinTiles,
                                 kHeavyMeanFactor, kHeavyMaxWindowsNat};
@@ -1003,28 +1051,22 @@ static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const
                            large, medium, list_l, list_m, counts, listed);
         hipLaunchKernelGGL(heavy_list, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
                            large, medium, counts, list_l, list_m, listed);
+        hipLaunchKernelGGL(heavy_sort, dim3(1), dim3(kHeavyMaxWindows), 0, st, d_window_offsets,
+                           W, list_l);
         const hipError_t le = hipGetLastError();
-        f3s_status s =
-            le == hipSuccess ? F3S_OK : hip_fail(le, "heavy window lists", __FILE__, __LINE__);
-        for (int c = 0; c < 2 && s == F3S_OK; ++c) {
-            const HeavyClass& hc = c == 0 ? large : medium;
-            AttnParams ph = p;
-            ph.window_order = c == 0 ? list_l : list_m;
-            ph.xcd_contiguous = 0;
-            ph.team = c == 0 ? kTeamLarge : kTeamSmall;
-            ph.num_items = (int64_t)hc.cap * ph.team;
-            ph.heavy_mode = 2;
-            ph.heavy_max = hc.cap;
-            ph.heavy_min = hc.lo_min;
-            ph.heavy_factor = hc.lo_factor;
-            s = launch(ph, H, scale, st);
-        }
-        if (s == F3S_OK) {
-            p.heavy_mode = 3;
-            p.heavy_listed = listed;
-            s = launch(p, H, scale, st);
-        }
-        return s;
+        if (le != hipSuccess) return hip_fail(le, "heavy window lists", __FILE__, __LINE__);
+        AttnParams ph = p;
+        ph.window_order = list_l;
+        ph.xcd_contiguous = 0;
+        ph.team = kTeamLarge;
+        ph.num_items = (int64_t)large.cap * kTeamLarge;
+        F3S_TRY(launch(ph, H, scale, st));
+        p.heavy_mode = 3;
+        p.heavy_listed = listed;
+        p.prefix_list = list_m;
+        p.prefix_items = medium.cap;
+        p.num_items = (int64_t)medium.cap + W;
+        return launch(p, H, scale, st);
     }
     if (p.team == 1 && d_window_order && !wide_features(n, H)) {
         // Without a plan a hub window would run on one wave.  Given a window

@@ -136,12 +136,13 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * graphs, given d_window_order, the heavy windows among its first 512
  * entries (more than max(1024, 8 x mean) tiles) run as teams of 16 in a
  * launch of their own before the others; in natural order, the first 512
- * windows of more than max(1024, 8 x mean) tiles run as teams of 16 and the
- * first 4,096 of more than max(512, 2 x mean) (but not more than the first
- * bound) as teams of 4, listed by two small kernels into a few tens of KB of
- * scratch taken from the library's pool and returned to it in stream order
- * on `stream` (the call does not wait).  Every other path allocates
- * nothing. */
+ * windows of more than max(1024, 8 x mean) tiles run as teams of 16,
+ * heaviest first, and the first 4,096 of more than max(512, 2 x mean) (but
+ * not more than the first bound) start the one-wave launch, ahead of the
+ * other windows in index order -- listed and sorted by three small kernels
+ * into a few tens of KB of scratch taken from the library's pool and
+ * returned to it in stream order on `stream` (the call does not wait).
+ * Every other path allocates nothing. */
 f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                              float* O, const int32_t* d_window_offsets,
                              const int32_t* d_block_col, const uint16_t* d_tile_mask,

@@ -563,12 +563,12 @@ def test_unplanned_heavy_windows(gpu):
 
 
 def test_unplanned_natural_order_heavy_cap(gpu):
-    # Natural order gives the first 4,096 windows by index of more than
-    # max(512, 2 x mean) tiles (and no more than max(1024, 8 x mean)) to a
-    # launch of 4-wave teams.  Here
+    # Natural order starts the one-wave launch with the first 4,096 windows
+    # by index of more than max(512, 2 x mean) tiles (and no more than
+    # max(1024, 8 x mean)), the rest following in index order.  Here
     # 4,200 windows (every 4th of 16,800) hold exactly 600 tiles: the last
-    # 104 run on one wave each, and the listing kernels' 256-window blocks
-    # each hold 64 of them.  With a window order the rule is max(1024,
+    # 104 are not listed and run in their index position, and the listing
+    # kernels' 256-window blocks each hold 64 of them.  With a window order the rule is max(1024,
     # 8 x mean) = 1,208 tiles, so no window is heavy there.  Results meet the
     # oracle; repeated runs give the same bits.
     W = 16_800
