@@ -525,6 +525,7 @@ def main() -> int:
         print("[bench] timing the reference's semantics and launch shapes ...", file=sys.stderr,
               flush=True)
         sorted_order = order if use_sorted else f3s.window_order_device(bsf, stream)
+        occ_masked = occ_sum if masked else f3s.bsf_stats(bsf, True, stream)[0]
         ref_plan = plan if plan is not None else make_plan()
         rps = ref_plan.stats()
         legs = {}
@@ -535,9 +536,12 @@ def main() -> int:
             t = time_passes(f3s, fn, stream, reps)
             mean = float(t.mean())
             b = compulsory_bytes(n, H, bsf.W, bsf.T, kv_rows[sem_masked], sem_masked, lnch, rps)
+            rows = 2 * H * (occ_masked if sem_masked else bsf.T * 16)
             legs[name] = {"kernel_us": mean * 1e3, "edges_per_s": nnz / (mean * 1e-3),
                           "passes": reps, "compulsory_bytes": b,
-                          "roofline_frac": b / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS}
+                          "roofline_frac": b / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                          "gathered_rows_per_s": rows / (mean * 1e-3),
+                          "over_gather_ceiling": rows / (mean * 1e-3) / gc["rows_per_s"]}
 
         leg("tile_dense_planned",
             lambda: ref_plan.forward(dQ, dK, dV, dO, masked=False, stream=stream),
