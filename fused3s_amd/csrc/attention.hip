@@ -91,8 +91,7 @@ fused_attention_kernel(const AttnParams p)
     int64_t item_idx;
     int h;
     if constexpr (TEAM == 1) {
-        const uint32_t gw =
-            (uint32_t)(logical_block(p.xcd_contiguous, p.prefix_blocks) * WPG + wave);
+        const uint32_t gw = (uint32_t)(logical_block(p.xcd_contiguous) * WPG + wave);
         item_idx = (int64_t)(gw / (uint32_t)H);
         h = (int)(gw % (uint32_t)H);
     } else {
@@ -120,28 +119,18 @@ fused_attention_kernel(const AttnParams p)
         }
     } else {
         const int64_t wi = item_idx / TEAM;
-        if (p.heavy_mode == 3) {
-            // natural order: the listed medium windows first, then every
-            // window not listed (the team launch took the large ones)
-            if (wi < p.prefix_items) {
-                w = p.prefix_list[wi];
-            } else {
-                w = (int32_t)(wi - p.prefix_items);
-                if (w < p.W && ((p.heavy_listed[w >> 5] >> (w & 31)) & 1u)) return;
-            }
-        } else {
-            w = p.window_order ? p.window_order[wi] : (int32_t)wi;
-        }
-        if (w < 0 || w >= p.W) return;
+        w = p.window_order ? p.window_order[wi] : (int32_t)wi;
+        if (w < 0 || w >= p.W) return;   // an empty slot or an invalid order entry
         const int32_t T = p.window_offsets[p.W];
         tb = max(0, min(p.window_offsets[w], T));
         te = max(tb, min(p.window_offsets[w + 1], T));
-        if (p.heavy_mode == 1 || p.heavy_mode == 2) {
-            // the heavy windows among the first heavy_max order positions
-            // belong to the team launch (mode 2), all others to the one-wave
-            // launch (mode 1); uniform over a team's workgroup
+        if (p.heavy_mode) {
+            // in an order's sequence, the heavy windows among its first
+            // kHeavyMaxWindows entries belong to the team launch (mode 2), all
+            // others to the one-wave launch (mode 1); uniform over a team
             const bool heavy =
-                wi < p.heavy_max && te - tb > heavy_tiles(T, p.W, p.heavy_min, p.heavy_factor);
+                wi < kHeavyMaxWindows &&
+                te - tb > heavy_tiles(T, p.W, kHeavyMinTiles, kHeavyMeanFactor);
             if (heavy != (p.heavy_mode == 2)) return;
         }
         if constexpr (TEAM > 1) {
@@ -781,16 +770,12 @@ static void launch_mw(const AttnParams& p, int64_t waves, hipStream_t st)
         }
     }
     // Small launches use one-wave workgroups so they spread over all CUs.
-    // Prefix items fill whole workgroups: prefix_items * H is a multiple of 32.
-    AttnParams q = p;
     if (waves < 4 * 256 * 2) {
-        q.prefix_blocks = q.prefix_items * q.H;
         hipLaunchKernelGGL((fused_attention_kernel<MODE, 1, WIDE, 1>), dim3((unsigned)waves),
-                           dim3(kWave), 0, st, q);
+                           dim3(kWave), 0, st, p);
     } else {
-        q.prefix_blocks = q.prefix_items * q.H / 4;
         hipLaunchKernelGGL((fused_attention_kernel<MODE, 4, WIDE, 1>),
-                           dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, q);
+                           dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
     }
     if (p.num_split > 0)
         hipLaunchKernelGGL(merge_partials_kernel,
@@ -806,18 +791,54 @@ static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
         launch_mw<MODE, false>(p, waves, st);
 }
 
-// Natural-order unplanned launches: the heavy windows of a class (more tiles
-// than the class threshold and, for the medium class, no more than the large
-// threshold), the first `cap` of them by index (deterministic), as a list
-// (entries past the count stay -1, which the launches skip) -- the large
-// class for the team launch, the medium class for the one-wave launch to
-// start first -- and as bits of a bitmap the rest of the one-wave launch
-// skips.  Blocks of 256 windows cover whole bitmap words.
-struct HeavyClass {
-    int32_t lo_min, lo_factor;   // in the class: more tiles than max(lo_min, lo_factor x mean)
-    int32_t hi_min, hi_factor;   // ... and, if hi_min > 0, no more than max(hi_min, hi_factor x mean)
-    int32_t cap;                 // list entries
+// ---------------------------------------------------------------------------
+// Schedule of the unplanned launch on graphs of more than kHeavyMaxWindows
+// windows, in natural order and, from kSchedOrderedMin window-heads on, with
+// a window order too.  The order then only names the windows to compute
+// (each named window once; invalid entries are skipped, unnamed windows left
+// untouched); the schedule is the library's own, whatever the order:
+//   * heavy windows -- more than max(kHeavyMinTiles, kHeavyMeanFactor x mean)
+//     tiles -- heaviest first; the first kHeavyMaxWindows of them run as
+//     16-wave teams in a launch of their own;
+//   * every other window on one wave, by class of tile count (the octave;
+//     heavy windows past the team list form the first classes), heaviest
+//     class first, each class in index order and cut into eight contiguous
+//     shares, one per XCD.  XCD x runs its share of every class in class
+//     order: the longest windows start first and only the smallest finish
+//     last, and each XCD walks a contiguous range of windows within a class,
+//     which keeps a community-ordered graph's neighbours in its L2.
+// Four small kernels build it, and no memory needs clearing first (so the
+// launch may be captured into a graph): sched_inverse (an order's inverse,
+// scattered: window w is named iff inv[w] is a position that holds w, which
+// no stale value of an unnamed entry can fake), sched_count (per-block class
+// counts), sched_scan (one workgroup: class offsets, the team list's part of
+// each class, the XCD tables) and sched_fill (each window's slot, and -1 in
+// every slot no window takes).  Class positions q run 0 (heaviest class) to
+// kSchedClasses - 1.
+constexpr int kSchedClasses = 64;   // 32 octaves of the tile count, x {heavy, not}
+// A window order's sequence is replaced by the schedule from this many
+// window-heads on (W x H): the schedule's four small kernels cost ~30 us per
+// call, 5 % of config 4's pass (62,500 window-heads, which keeps the order's
+// sequence) and under 1.5 % from here on.
+constexpr int64_t kSchedOrderedMin = (int64_t)1 << 18;
+constexpr int kSchedBlock = 256;    // windows per block of sched_count / sched_fill
+
+struct SchedTables {
+    int32_t size[kSchedClasses];               // windows per class outside the team list
+    int32_t taken[kSchedClasses];              // windows per class in the team list
+    int32_t team_base[kSchedClasses];          // team-list position of a class's first window
+    int32_t xcd_base[kXcds][kSchedClasses];    // XCD x's slots before its share of a class
+    int32_t xcd_items[kXcds];                  // XCD x's slots in use
+    int32_t team_items;                        // team-list entries in use
 };
+
+// Slots per XCD in the one-wave launch: past any XCD's share of W windows
+// (each class share rounds up by at most one), a multiple of 4 so that every
+// XCD's slots fill whole 4-wave workgroups.
+constexpr int64_t sched_xcd_slots(int64_t W)
+{
+    return (ceil_div(W, kXcds) + kSchedClasses + 3) / 4 * 4;
+}
 
 // Tiles of window w (-1 past the last window).
 __device__ __forceinline__ int32_t window_tiles(const int32_t* __restrict__ window_offsets,
@@ -830,130 +851,175 @@ __device__ __forceinline__ int32_t window_tiles(const int32_t* __restrict__ wind
     return te - tb;
 }
 
-__device__ __forceinline__ bool heavy_in_class(int32_t t, int32_t T, int32_t W, const HeavyClass& hc)
+// Class position of window w (-1: past W, or not named by the order).
+__device__ __forceinline__ int sched_pos(const int32_t* __restrict__ window_offsets,
+                                         const int32_t* __restrict__ order,
+                                         const int32_t* __restrict__ inv, int32_t W, int32_t w,
+                                         int32_t heavy)
 {
-    return t > heavy_tiles(T, W, hc.lo_min, hc.lo_factor) &&
-           (hc.hi_min <= 0 || t <= heavy_tiles(T, W, hc.hi_min, hc.hi_factor));
-}
-
-// heavy_count: per block, the number of its windows in each of two disjoint
-// classes (counts[b] for a, counts[nb + b] for b); block 0 fills both lists
-// with -1, and each block zeroes its bitmap words.
-__global__ void __launch_bounds__(256)
-heavy_count(const int32_t* __restrict__ window_offsets, int32_t W, HeavyClass a, HeavyClass b,
-            int32_t* __restrict__ list_a, int32_t* __restrict__ list_b,
-            int32_t* __restrict__ counts, uint32_t* __restrict__ listed)
-{
-    const int32_t w = blockIdx.x * 256 + threadIdx.x;
-    if (blockIdx.x == 0) {
-        for (int i = threadIdx.x; i < a.cap; i += 256) list_a[i] = -1;
-        for (int i = threadIdx.x; i < b.cap; i += 256) list_b[i] = -1;
+    if (w >= W) return -1;
+    if (order) {
+        const int32_t p = inv[w];
+        if (p < 0 || p >= W || order[p] != w) return -1;
     }
-    if (threadIdx.x < 8 && (int64_t)blockIdx.x * 8 + threadIdx.x < ((int64_t)W + 31) / 32)
-        listed[blockIdx.x * 8 + threadIdx.x] = 0u;
-    const int32_t T = W > 0 ? window_offsets[W] : 0;
     const int32_t t = window_tiles(window_offsets, W, w);
-    const bool in_a = t >= 0 && heavy_in_class(t, T, W, a);
-    const bool in_b = t >= 0 && heavy_in_class(t, T, W, b);
-    __shared__ int32_t wc[2][4];
-    const int32_t ca = __popcll(__ballot(in_a));
-    const int32_t cb = __popcll(__ballot(in_b));
-    if ((threadIdx.x & (kWave - 1)) == 0) {
-        wc[0][threadIdx.x / kWave] = ca;
-        wc[1][threadIdx.x / kWave] = cb;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        counts[blockIdx.x] = wc[0][0] + wc[0][1] + wc[0][2] + wc[0][3];
-        counts[gridDim.x + blockIdx.x] = wc[1][0] + wc[1][1] + wc[1][2] + wc[1][3];
-    }
+    const int oct = t > 0 ? 32 - __clz(t) : 0;   // t < 2^31: 0..31
+    return t > heavy ? 31 - oct : kSchedClasses - 1 - oct;
 }
 
-// heavy_list: a window's rank in its class is the class's windows in earlier
-// blocks plus those before it in its block; ranks below the class's cap are
-// listed and their bits set in the bitmap (one lane per word).
-__global__ void __launch_bounds__(256)
-heavy_list(const int32_t* __restrict__ window_offsets, int32_t W, HeavyClass a, HeavyClass b,
-           const int32_t* __restrict__ counts, int32_t* __restrict__ list_a,
-           int32_t* __restrict__ list_b, uint32_t* __restrict__ listed)
+__global__ void __launch_bounds__(kSchedBlock)
+sched_inverse(const int32_t* __restrict__ order, int32_t W, int32_t* __restrict__ inv)
 {
-    __shared__ int32_t red[2][4];
-    __shared__ int32_t wc[2][4];
-    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
-    int32_t before_a = 0, before_b = 0;
-    for (int32_t k = threadIdx.x; k < (int32_t)blockIdx.x; k += 256) {
-        before_a += counts[k];
-        before_b += counts[gridDim.x + k];
-    }
-    before_a = wave_sum(before_a);
-    before_b = wave_sum(before_b);
-    if (lane == 0) {
-        red[0][wid] = before_a;
-        red[1][wid] = before_b;
-    }
-    __syncthreads();
-    before_a = red[0][0] + red[0][1] + red[0][2] + red[0][3];
-    before_b = red[1][0] + red[1][1] + red[1][2] + red[1][3];
-    if (before_a >= a.cap && before_b >= b.cap) return;   // uniform
-    const int32_t w = blockIdx.x * 256 + threadIdx.x;
-    const int32_t T = W > 0 ? window_offsets[W] : 0;
-    const int32_t t = window_tiles(window_offsets, W, w);
-    const bool in_a = t >= 0 && heavy_in_class(t, T, W, a);
-    const bool in_b = t >= 0 && heavy_in_class(t, T, W, b);
-    const uint64_t bal_a = __ballot(in_a);
-    const uint64_t bal_b = __ballot(in_b);
-    if (lane == 0) {
-        wc[0][wid] = __popcll(bal_a);
-        wc[1][wid] = __popcll(bal_b);
-    }
-    __syncthreads();
-    const uint64_t below = (1ull << lane) - 1ull;
-    int32_t rank_a = before_a + __popcll(bal_a & below);
-    int32_t rank_b = before_b + __popcll(bal_b & below);
-    for (int v = 0; v < wid; ++v) {
-        rank_a += wc[0][v];
-        rank_b += wc[1][v];
-    }
-    const bool take_a = in_a && rank_a < a.cap;
-    const bool take_b = in_b && rank_b < b.cap;
-    if (take_a) list_a[rank_a] = w;
-    if (take_b) list_b[rank_b] = w;
-    // each wave owns its two bitmap words
-    const uint64_t tb = __ballot(take_a || take_b);
-    const int64_t word = ((int64_t)blockIdx.x * 256 + wid * kWave) / 32;
-    if (lane == 0 && word < ((int64_t)W + 31) / 32) listed[word] = (uint32_t)tb;
-    if (lane == 1 && word + 1 < ((int64_t)W + 31) / 32) listed[word + 1] = (uint32_t)(tb >> 32);
+    const int32_t p = blockIdx.x * kSchedBlock + threadIdx.x;
+    if (p >= W) return;
+    const int32_t w = order[p];
+    if (w >= 0 && w < W) inv[w] = p;   // duplicates: any of their positions
 }
 
-// heavy_sort (one workgroup): the team launch's list heaviest first (ties by
-// index; empty entries last), so the dispatcher starts the longest windows
-// first, as the reference's descending order does.
-static_assert(kHeavyMaxWindows == 512, "heavy_sort sorts 512 entries, one per thread");
-__global__ void __launch_bounds__(512)
-heavy_sort(const int32_t* __restrict__ window_offsets, int32_t W, int32_t* __restrict__ list)
+__global__ void __launch_bounds__(kSchedBlock)
+sched_count(const int32_t* __restrict__ window_offsets, const int32_t* __restrict__ order,
+            const int32_t* __restrict__ inv, int32_t W, int32_t nb, int32_t* __restrict__ counts)
 {
-    __shared__ uint64_t key[kHeavyMaxWindows];
+    __shared__ int32_t hist[kSchedClasses];
     const int t = threadIdx.x;
-    const int32_t w = list[t];
-    const int32_t tiles = (w >= 0 && w < W) ? window_tiles(window_offsets, W, w) : -1;
-    key[t] = tiles >= 0 ? ((uint64_t)(uint32_t)(0x7fffffff - tiles) << 32) | (uint32_t)w
-                        : ~0ull;
+    if (t < kSchedClasses) hist[t] = 0;
     __syncthreads();
-    for (int size = 2; size <= kHeavyMaxWindows; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const int u = t ^ stride;
-            if (u > t) {
-                const uint64_t a = key[t], b = key[u];
-                if ((a > b) == ((t & size) == 0)) {
-                    key[t] = b;
-                    key[u] = a;
-                }
-            }
-            __syncthreads();
+    const int32_t heavy = heavy_tiles(window_offsets[W], W, kHeavyMinTiles, kHeavyMeanFactor);
+    const int q = sched_pos(window_offsets, order, inv, W, blockIdx.x * kSchedBlock + t, heavy);
+    if (q >= 0) atomicAdd(&hist[q], 1);
+    __syncthreads();
+    if (t < kSchedClasses) counts[(int64_t)t * nb + blockIdx.x] = hist[t];
+}
+
+// One workgroup of 1,024 threads: counts[q][b] becomes the class-q windows in
+// blocks before b; then the tables.  The counts were written by other XCDs a
+// kernel earlier, so every load goes below L2: each class's row is cut into
+// 16 contiguous segments, one per lane of a 16-lane row, and a lane loads its
+// segment in one batch (kept in registers for the rewrite when it holds at
+// most kSegRegs values: graphs of up to 131,072 windows), scans the
+// 16 sums with its row and writes its segment's offsets.  The tables come
+// from wave-wide scans over the classes.
+constexpr int kScanSegs = 16;
+constexpr int kSegRegs = 32;
+static_assert(kSchedClasses * kScanSegs == 1024, "one lane per (class, segment)");
+static_assert(kSchedClasses == kWave, "one lane per class in the table scans");
+__global__ void __launch_bounds__(1024)
+sched_scan(int32_t* __restrict__ counts, int32_t nb, SchedTables* __restrict__ tab)
+{
+    __shared__ int32_t total[kSchedClasses];
+    __shared__ int32_t size[kSchedClasses];
+    const int q = threadIdx.x / kScanSegs, k = threadIdx.x % kScanSegs;
+    const int lane = threadIdx.x % kWave, wid = threadIdx.x / kWave;
+    const int32_t seg = (nb + kScanSegs - 1) / kScanSegs;
+    const int32_t b0 = min(nb, k * seg), b1 = min(nb, b0 + seg);
+    int32_t* row = counts + (int64_t)q * nb;
+    int32_t sum = 0;
+    int32_t v[kSegRegs];
+    if (seg <= kSegRegs) {   // uniform
+#pragma unroll
+        for (int u = 0; u < kSegRegs; ++u) v[u] = b0 + u < b1 ? row[b0 + u] : 0;
+#pragma unroll
+        for (int u = 0; u < kSegRegs; ++u) sum += v[u];
+    } else {
+        for (int32_t b = b0; b < b1; b += kSegRegs) {
+#pragma unroll
+            for (int u = 0; u < kSegRegs; ++u) v[u] = b + u < b1 ? row[b + u] : 0;
+#pragma unroll
+            for (int u = 0; u < kSegRegs; ++u) sum += v[u];
         }
     }
-    const uint64_t k = key[t];
-    list[t] = k == ~0ull ? -1 : (int32_t)(uint32_t)k;
+    int32_t inc = sum;
+#pragma unroll
+    for (int off = 1; off < kScanSegs; off <<= 1) {
+        const int32_t y = __shfl_up(inc, off, kScanSegs);
+        if (k >= off) inc += y;
+    }
+    if (k == kScanSegs - 1) total[q] = inc;
+    int32_t run = inc - sum;
+    if (seg <= kSegRegs) {
+#pragma unroll
+        for (int u = 0; u < kSegRegs; ++u) {
+            if (b0 + u < b1) row[b0 + u] = run;
+            run += v[u];
+        }
+    } else {
+        for (int32_t b = b0; b < b1; b += kSegRegs) {
+#pragma unroll
+            for (int u = 0; u < kSegRegs; ++u) v[u] = b + u < b1 ? row[b + u] : 0;
+#pragma unroll
+            for (int u = 0; u < kSegRegs; ++u) {
+                if (b + u < b1) row[b + u] = run;
+                run += v[u];
+            }
+        }
+    }
+    __syncthreads();
+    if (wid == 0) {
+        // lane = class: the heavy classes come first, and the team list takes
+        // their first kHeavyMaxWindows windows
+        const int32_t tot = total[lane];
+        const int32_t heavy = lane < kSchedClasses / 2 ? tot : 0;
+        const int32_t before = wave_inclusive_scan(heavy) - heavy;
+        const int32_t take = max(0, min(heavy, kHeavyMaxWindows - before));
+        const int32_t team_all = min(kHeavyMaxWindows, __shfl(before + heavy, kWave - 1));
+        tab->team_base[lane] = lane < kSchedClasses / 2 ? min(before, kHeavyMaxWindows) : team_all;
+        tab->taken[lane] = take;
+        tab->size[lane] = size[lane] = tot - take;
+        if (lane == 0) tab->team_items = team_all;
+    }
+    __syncthreads();
+    if (wid < kXcds) {
+        // wave x: XCD x's share of each class, scanned over the classes
+        const int64_t x = wid, sc = size[lane];
+        const int32_t share = (int32_t)(sc * (x + 1) / kXcds - sc * x / kXcds);
+        const int32_t incl = wave_inclusive_scan(share);
+        tab->xcd_base[x][lane] = incl - share;
+        if (lane == kWave - 1) tab->xcd_items[x] = incl;
+    }
+}
+
+// Slots: the team list (kHeavyMaxWindows entries) and, per XCD, L one-wave
+// slots; a class's windows keep their index order (stable ranks within a
+// block from wave ballots).
+__global__ void __launch_bounds__(kSchedBlock)
+sched_fill(const int32_t* __restrict__ window_offsets, const int32_t* __restrict__ order,
+           const int32_t* __restrict__ inv, int32_t W, int32_t nb,
+           const int32_t* __restrict__ counts, const SchedTables* __restrict__ tab, int32_t L,
+           int32_t* __restrict__ team, int32_t* __restrict__ sched)
+{
+    __shared__ int32_t wc[kSchedBlock / kWave][kSchedClasses];
+    const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
+    const int64_t g = (int64_t)blockIdx.x * kSchedBlock + t;
+    if (g < (int64_t)kXcds * L && g % L >= tab->xcd_items[g / L]) sched[g] = -1;
+    if (g < kHeavyMaxWindows && g >= tab->team_items) team[g] = -1;
+    if ((int32_t)blockIdx.x >= nb) return;   // uniform
+    const int32_t heavy = heavy_tiles(window_offsets[W], W, kHeavyMinTiles, kHeavyMeanFactor);
+    const int32_t w = blockIdx.x * kSchedBlock + t;
+    const int q = sched_pos(window_offsets, order, inv, W, w, heavy);
+    for (int k = lane; k < kSchedClasses; k += kWave) wc[wid][k] = 0;
+    int32_t rank = 0;
+    const uint64_t below = (1ull << lane) - 1ull;
+    uint64_t rem = __ballot(q >= 0);
+    while (rem) {   // one round per class present in the wave
+        const int lead = __ffsll((unsigned long long)rem) - 1;
+        const int cq = __shfl(q, lead);
+        const uint64_t m = __ballot(q == cq);
+        if (q == cq) rank = __popcll(m & below);
+        if (lane == lead) wc[wid][cq] = __popcll(m);
+        rem &= ~m;
+    }
+    __syncthreads();
+    if (q < 0) return;
+    for (int v = 0; v < wid; ++v) rank += wc[v][q];
+    const int32_t r = counts[(int64_t)q * nb + blockIdx.x] + rank;   // rank in its class
+    const int32_t take = tab->taken[q];
+    if (r < take) {
+        team[tab->team_base[q] + r] = w;
+        return;
+    }
+    const int64_t sz = tab->size[q], r2 = r - take;
+    const int64_t x = (kXcds * r2 + kXcds - 1) / sz;   // its share: [sz x / 8, sz (x + 1) / 8)
+    sched[x * L + tab->xcd_base[x][q] + (r2 - sz * x / kXcds)] = w;
 }
 
 static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
@@ -981,17 +1047,28 @@ static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
     return F3S_OK;
 }
 
-// Bytes of the natural-order launch's scratch for W windows: the two heavy
-// window lists, two per-block counts per 256 windows and the bitmap of the
-// listed windows.
-static size_t natural_scratch_bytes(int64_t W)
+// Scratch of the scheduled launch for W windows, in 256-byte sections: the
+// tables, the team list, the class counts (kSchedClasses per block of
+// kSchedBlock windows), the one-wave slots and, given a window order, its
+// inverse.
+struct SchedScratch {
+    size_t tab, team, counts, sched, inv, bytes;
+};
+constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+constexpr SchedScratch sched_scratch(int64_t W, bool ordered)
 {
-    const int64_t nb = ceil_div(W, 256), words = ceil_div(W, 32);
-    return sizeof(int32_t) * ((size_t)kHeavyMaxWindows + kHeavyMaxWindowsNat + 2 * (size_t)nb) +
-           sizeof(uint32_t) * (size_t)words;
+    auto up = round256;
+    SchedScratch l{};
+    l.tab = 0;
+    l.team = up(sizeof(SchedTables));
+    l.counts = l.team + up(sizeof(int32_t) * kHeavyMaxWindows);
+    l.sched = l.counts + up(sizeof(int32_t) * kSchedClasses * (size_t)ceil_div(W, kSchedBlock));
+    l.inv = l.sched + up(sizeof(int32_t) * kXcds * (size_t)sched_xcd_slots(W));
+    l.bytes = l.inv + (ordered ? up(sizeof(int32_t) * (size_t)W) : 0);
+    return l;
 }
 
-// f3s_attention_fwd; the natural-order launch takes its scratch from
+// f3s_attention_fwd; the scheduled launch takes its scratch from
 // `fixed_scratch` when given (f3s_attention_fwd_noalloc, already checked to
 // be large enough), else from the allocator, returned in stream order.
 static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
@@ -1023,72 +1100,57 @@ static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const
     p.n = n;
     p.xcd_contiguous = d_window_order == nullptr;
     hipStream_t st = as_stream(stream);
-    if (p.team == 1 && !d_window_order && !wide_features(n, H) && W > kHeavyMaxWindows) {
-        // Natural order: the hubs can be anywhere.  Two small kernels list the
-        // large windows (the ordered rule) and the medium ones, in a few tens
-        // of KB of scratch, and a third sorts the large ones heaviest first
-        // for a launch of 16-wave teams; the one-wave launch then starts the
-        // medium windows (dealt round-robin to the XCDs) before all others,
-        // which follow in natural order, XCD-contiguous, skipping the listed
-        // windows.  (Teams of 4 for the medium windows measured slower: their
-        // launch cannot start before the large teams' ends.)
-        const HeavyClass large{kHeavyMinTiles, kHeavyMeanFactor, 0, 0, kHeavyMaxWindows};
-        const HeavyClass medium{kHeavyMinTilesNat, kHeavyMeanFactorNat, kHeavyMinTiles,
-                                kHeavyMeanFactor, kHeavyMaxWindowsNat};
-        const int32_t nb = (int32_t)ceil_div(W, 256);
-        // every word of it is written by heavy_count before it is read
+    const bool ordered = d_window_order != nullptr;
+    if (p.team == 1 && !wide_features(n, H) && W > kHeavyMaxWindows &&
+        (!ordered || (int64_t)W * H >= kSchedOrderedMin)) {
+        // the library's schedule (see sched_fill): heavy windows on teams of
+        // 16 waves, the others on one wave each, by class, XCD by XCD
+        const SchedScratch lay = sched_scratch(W, ordered);
         StreamBuffer scratch(st);   // returned to the allocator in stream order, after the launches
-        void* sp = fixed_scratch;
+        char* sp = static_cast<char*>(fixed_scratch);
         if (!sp) {
-            F3S_TRY(scratch.reserve(natural_scratch_bytes(W)));
-            sp = scratch.ptr;
+            F3S_TRY(scratch.reserve(lay.bytes));
+            sp = static_cast<char*>(scratch.ptr);
         }
-        int32_t* list_l = reinterpret_cast<int32_t*>(sp);
-        int32_t* list_m = list_l + large.cap;
-        int32_t* counts = list_m + medium.cap;   // 2 x nb
-        uint32_t* listed = reinterpret_cast<uint32_t*>(counts + 2 * nb);
-        hipLaunchKernelGGL(heavy_count, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
-                           large, medium, list_l, list_m, counts, listed);
-        hipLaunchKernelGGL(heavy_list, dim3((unsigned)nb), dim3(256), 0, st, d_window_offsets, W,
-                           large, medium, counts, list_l, list_m, listed);
-        hipLaunchKernelGGL(heavy_sort, dim3(1), dim3(kHeavyMaxWindows), 0, st, d_window_offsets,
-                           W, list_l);
+        SchedTables* tab = reinterpret_cast<SchedTables*>(sp + lay.tab);
+        int32_t* team = reinterpret_cast<int32_t*>(sp + lay.team);
+        int32_t* counts = reinterpret_cast<int32_t*>(sp + lay.counts);
+        int32_t* sched = reinterpret_cast<int32_t*>(sp + lay.sched);
+        int32_t* inv = ordered ? reinterpret_cast<int32_t*>(sp + lay.inv) : nullptr;
+        const int32_t nb = (int32_t)ceil_div(W, kSchedBlock);
+        const int64_t L = sched_xcd_slots(W);
+        const int32_t fill_blocks = (int32_t)std::max<int64_t>(nb, ceil_div(kXcds * L, kSchedBlock));
+        if (ordered)
+            hipLaunchKernelGGL(sched_inverse, dim3((unsigned)nb), dim3(kSchedBlock), 0, st,
+                               d_window_order, W, inv);
+        hipLaunchKernelGGL(sched_count, dim3((unsigned)nb), dim3(kSchedBlock), 0, st,
+                           d_window_offsets, d_window_order, inv, W, nb, counts);
+        hipLaunchKernelGGL(sched_scan, dim3(1), dim3(1024), 0, st, counts, nb, tab);
+        hipLaunchKernelGGL(sched_fill, dim3((unsigned)fill_blocks), dim3(kSchedBlock), 0, st,
+                           d_window_offsets, d_window_order, inv, W, nb, counts, tab, (int32_t)L,
+                           team, sched);
         const hipError_t le = hipGetLastError();
-        if (le != hipSuccess) return hip_fail(le, "heavy window lists", __FILE__, __LINE__);
+        if (le != hipSuccess) return hip_fail(le, "window schedule", __FILE__, __LINE__);
         AttnParams ph = p;
-        ph.window_order = list_l;
+        ph.window_order = team;
         ph.xcd_contiguous = 0;
         ph.team = kTeamLarge;
-        ph.num_items = (int64_t)large.cap * kTeamLarge;
+        ph.num_items = (int64_t)kHeavyMaxWindows * kTeamLarge;
         F3S_TRY(launch(ph, H, scale, st));
-        p.heavy_mode = 3;
-        p.heavy_listed = listed;
-        p.prefix_list = list_m;
-        p.prefix_items = medium.cap;
-        p.num_items = (int64_t)medium.cap + W;
-        return launch(p, H, scale, st);
-    }
-    if (p.team == 1 && d_window_order && !wide_features(n, H)) {
-        // Without a plan a hub window would run on one wave.  Given a window
-        // order, two launches instead: teams of 16 waves for the heavy
-        // windows among the first kHeavyMaxWindows order positions (the
-        // reference's descending order puts the hubs there), then one wave
-        // per window for all others.  Each window belongs to exactly one
-        // launch whatever the order.  (In natural order the hubs are
-        // anywhere, and the extra launch measured a little slower.)
-        const int32_t K = W < kHeavyMaxWindows ? W : kHeavyMaxWindows;
+        p.window_order = sched;
+        p.xcd_contiguous = 1;
+        p.num_items = kXcds * L;
+    } else if (p.team == 1 && ordered && !wide_features(n, H)) {
+        // The order's sequence: teams of 16 waves for the heavy windows among
+        // its first kHeavyMaxWindows entries (the reference's descending order
+        // puts the hubs there), then one wave per entry for all others; each
+        // entry belongs to exactly one of the two launches.
         AttnParams ph = p;
         ph.team = kTeamLarge;
-        ph.num_items = (int64_t)K * kTeamLarge;
+        ph.num_items = (int64_t)std::min<int32_t>(W, kHeavyMaxWindows) * kTeamLarge;
         ph.heavy_mode = 2;
-        ph.heavy_max = K;
-        ph.heavy_min = kHeavyMinTiles;
-        ph.heavy_factor = kHeavyMeanFactor;
         F3S_TRY(launch(ph, H, scale, st));
         p.heavy_mode = 1;
-        p.heavy_max = K;
-        p.heavy_min = kHeavyMinTiles;
-        p.heavy_factor = kHeavyMeanFactor;
     }
     return launch(p, H, scale, st);
 }
@@ -1096,18 +1158,15 @@ static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const
 
 // ------------------------------------------------ allocation-free entry point
 //
-// f3s_attention_fwd_noalloc: the natural-order launch's scratch (heavy
-// window lists, per-block counts, bitmap) lives in a file-scope device array
-// sized for graphs of up to kNoAllocMaxWindows row windows; each device holds
-// its own copy for the life of the process.  Host code never passes the
-// array's name to a kernel (on the host it is a stand-in, not a device
-// address): its device address is looked up once per device with
-// hipGetSymbolAddress and kept in g_noalloc_addr.
-constexpr int32_t kNoAllocMaxWindows = 1 << 22;   // n <= 67,108,864 nodes
-constexpr size_t kNoAllocScratchBytes =
-    (sizeof(int32_t) * ((size_t)kHeavyMaxWindows + kHeavyMaxWindowsNat +
-                        2 * (((size_t)kNoAllocMaxWindows + 255) / 256)) +
-     sizeof(uint32_t) * (((size_t)kNoAllocMaxWindows + 31) / 32) + 255) / 256 * 256;
+// f3s_attention_fwd_noalloc: the scheduled launch's scratch (tables, team
+// list, class counts, one-wave slots, an order's inverse) lives in a
+// file-scope device array sized for graphs of up to kNoAllocMaxWindows row
+// windows; each device holds its own copy for the life of the process.  Host
+// code never passes the array's name to a kernel (on the host it is a
+// stand-in, not a device address): its device address is looked up once per
+// device with hipGetSymbolAddress and kept in g_noalloc_addr.
+constexpr int32_t kNoAllocMaxWindows = 1 << 21;   // n <= 33,554,432 nodes
+constexpr size_t kNoAllocScratchBytes = sched_scratch(kNoAllocMaxWindows, true).bytes;
 static __device__ __align__(256) unsigned char noalloc_scratch[kNoAllocScratchBytes];
 
 constexpr int kNoAllocDevices = 64;
@@ -1169,20 +1228,17 @@ f3s_status f3s_attention_fwd_noalloc(const uint16_t* Q, const uint16_t* K, const
                                      int32_t d, int32_t H, float scale, void* stream)
 {
     if (W < 0 || W > kNoAllocMaxWindows) {
-        set_error("f3s_attention_fwd_noalloc: W outside [0, 4194304] (the limit of its fixed "
-                  "scratch, graphs of up to 67,108,864 nodes); use f3s_attention_fwd");
+        set_error("f3s_attention_fwd_noalloc: W outside [0, 2097152] (the limit of its fixed "
+                  "scratch, graphs of up to 33,554,432 nodes); use f3s_attention_fwd");
         return F3S_EUNSUPPORTED;
     }
     F3S_TRY(check_attention_args(Q, K, V, O, n, d, H));
     F3S_TRY(require_device());
     void* sp = nullptr;
     F3S_TRY(noalloc_scratch_addr(&sp));
-    static_assert(kNoAllocScratchBytes >= sizeof(int32_t) * (kHeavyMaxWindows + kHeavyMaxWindowsNat),
-                  "scratch holds the lists");
-    if (natural_scratch_bytes(W) > kNoAllocScratchBytes) {   // cannot happen for W <= max
-        set_error("f3s_attention_fwd_noalloc: scratch too small");
-        return F3S_EUNSUPPORTED;
-    }
+    static_assert(sched_scratch(kNoAllocMaxWindows, true).bytes >=
+                      sched_scratch(kNoAllocMaxWindows, false).bytes,
+                  "an order's inverse only adds to the scratch");
     return attention_fwd_impl(Q, K, V, O, d_window_offsets, d_block_col, d_tile_mask,
                               d_window_order, W, n, d, H, scale, stream, sp);
 }

@@ -82,36 +82,19 @@ struct AttnParams {
     const int32_t* chunk_base;       // compiled plan: item i owns chunks [cb[i], cb[i+1])
     const uint32_t* columns;         // compiled plan: per chunk 32 row offsets, 32 row masks
     int32_t team;                    // waves per window (1, or kTeamSmall / kTeamLarge)
-    int32_t heavy_mode;              // unplanned launches: 0 all windows; 1 all but the heavy
-                                     // windows among the first heavy_max order positions;
-                                     // 2 only those (teams); 3 natural order: the prefix
-                                     // windows first, then every window not set in
-                                     // heavy_listed
-    int32_t heavy_max;
-    int32_t heavy_min, heavy_factor; // heavy: more tiles than max(heavy_min, heavy_factor x mean)
-    const uint32_t* heavy_listed;    // heavy_mode 3: bitmap of the listed windows
-    const int32_t* prefix_list;      // heavy_mode 3: windows of items [0, prefix_items), -1 = none
-    int32_t prefix_items;            // heavy_mode 3: items taken from prefix_list
-    int32_t prefix_blocks;           // leading workgroups dealt round-robin to the XCDs even when
-                                     // xcd_contiguous is set (they hold the prefix items)
+    int32_t heavy_mode;              // order-sequence launches: 0 every entry; 1 all but the
+                                     // heavy windows among the first kHeavyMaxWindows
+                                     // entries; 2 only those (teams)
 };
 
-// A window is heavy for the unplanned team launch when its tiles exceed
-// both a minimum and a multiple of the mean window: given a window order,
-// kHeavyMinTiles and kHeavyMeanFactor, and only the first kHeavyMaxWindows
-// order positions (the reference's descending order puts the hubs there and
-// runs the other windows big-first); in natural order, the first
-// kHeavyMaxWindows such windows by index, run heaviest first.  Natural order
-// also lists the first kHeavyMaxWindowsNat windows below that bound but above
-// kHeavyMinTilesNat and kHeavyMeanFactorNat x mean: the one-wave launch
-// starts them before all others, since a window just under the team
-// threshold would otherwise start wherever its index puts it, possibly last.
+// A window is heavy for the unplanned launch's teams when its tiles exceed
+// both kHeavyMinTiles and kHeavyMeanFactor x the mean window; on the
+// library's schedule the first kHeavyMaxWindows of them (heaviest first),
+// in an order's sequence those among its first kHeavyMaxWindows entries, run
+// as 16-wave teams.
 constexpr int32_t kHeavyMinTiles = 1024;
 constexpr int32_t kHeavyMeanFactor = 8;
 constexpr int32_t kHeavyMaxWindows = 512;
-constexpr int32_t kHeavyMinTilesNat = 512;
-constexpr int32_t kHeavyMeanFactorNat = 2;
-constexpr int32_t kHeavyMaxWindowsNat = 4096;
 __host__ __device__ __forceinline__ int32_t heavy_tiles(int32_t T, int32_t W, int32_t min_tiles,
                                                         int32_t factor)
 {
@@ -161,16 +144,14 @@ static inline int32_t team_for(int64_t W, int32_t H, bool masked)
 // Workgroup index -> logical block.  The dispatcher deals workgroups to the
 // 8 XCDs round-robin; with `xcd_contiguous` each XCD instead receives one
 // contiguous range of logical blocks, so windows that share neighbours
-// (community-ordered graphs) share one XCD's L2.  The first `prefix` blocks (a
-// multiple of 8, so every later block keeps its XCD) stay round-robin: they
-// start first on every XCD.
-__device__ __forceinline__ int64_t logical_block(int32_t xcd_contiguous, int64_t prefix = 0)
+// (community-ordered graphs) share one XCD's L2.
+__device__ __forceinline__ int64_t logical_block(int32_t xcd_contiguous)
 {
     const int64_t b = blockIdx.x;
-    if (!xcd_contiguous || b < prefix) return b;
-    const int64_t G = gridDim.x - prefix, c = b - prefix;
-    const int64_t x = c % kXcds, q = G / kXcds, rem = G % kXcds;
-    return prefix + x * q + min(x, rem) + c / kXcds;
+    if (!xcd_contiguous) return b;
+    const int64_t G = gridDim.x;
+    const int64_t x = b % kXcds, q = G / kXcds, rem = G % kXcds;
+    return x * q + min(x, rem) + b / kXcds;
 }
 
 __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c)

@@ -23,7 +23,7 @@ f3s_status require_device();
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Device-wide exclusive scan of int32 counts into int64 (or int32) prefix
 // sums; out has count + 1 entries (out[count] = total).  tmp needs

@@ -124,25 +124,34 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
 
 /* f3s_1tb1rw_kernel (src/fused3s_v2.cu:81-90) and its launch
  * (tests/test_fused_3s_v2.cu:124-131): one fused pass, each row window
- * handled whole, windows taken in d_window_order (NULL = natural order).
+ * handled whole, over the windows d_window_order names (NULL = all).
  * O[i] = sum_j softmax_j(scale * Q[i].K[j]) V[j] per head; rows with no
- * attended column get 0.  Requires d == 64 and 1 <= H <= 64 heads in
- * node-major [n][H][64] layout, of any size (tensors past ~4 GiB are read
- * with 64-bit addresses); scale = 1 reproduces the reference (which has no
- * scaling, and one head).  Small graphs run each window on a team of 4 or
- * 16 waves of one workgroup (masked: W*H <= 1024, teams of 4; tile-dense:
- * W*H <= 512, teams of 16, up to 2048, teams of 4), each wave taking an even
- * share of the window's tiles, merged in LDS in a fixed order.  On larger
- * graphs, given d_window_order, the heavy windows among its first 512
- * entries (more than max(1024, 8 x mean) tiles) run as teams of 16 in a
- * launch of their own before the others; in natural order, the first 512
- * windows of more than max(1024, 8 x mean) tiles run as teams of 16,
- * heaviest first, and the first 4,096 of more than max(512, 2 x mean) (but
- * not more than the first bound) start the one-wave launch, ahead of the
- * other windows in index order -- listed and sorted by three small kernels
- * into a few tens of KB of scratch taken from the library's pool and
- * returned to it in stream order on `stream` (the call does not wait).
- * Every other path allocates nothing. */
+ * attended column get 0; rows of windows the order does not name are not
+ * written.  Requires d == 64 and 1 <= H <= 64 heads in node-major [n][H][64]
+ * layout, of any size (tensors past ~4 GiB are read with 64-bit addresses);
+ * scale = 1 reproduces the reference (which has no scaling, and one head).
+ * Small graphs run each window on a team of 4 or 16 waves of one workgroup
+ * (masked: W*H <= 1024, teams of 4; tile-dense: W*H <= 512, teams of 16, up
+ * to 2048, teams of 4), each wave taking an even share of the window's
+ * tiles, merged in LDS in a fixed order, in the order's sequence.  On larger
+ * graphs (W > 512), given d_window_order on a launch of fewer than 2^18
+ * window-heads (W x H), windows run in the order's sequence: the heavy
+ * windows (more than max(1024, 8 x mean) tiles) among its first 512 entries
+ * as teams of 16 waves in a launch of their own, every other entry on one
+ * wave.  In natural order, and with an order from 2^18 window-heads on, the
+ * order only names the windows -- each named window is computed once;
+ * invalid entries are skipped -- and the library schedules them itself,
+ * identically for every order: the heavy windows, heaviest first, the first
+ * 512 of them as teams of 16 waves in a launch of their own; every other
+ * window on one wave, by octave of its tile count, heaviest first, each
+ * octave in index order and cut into eight contiguous shares, one per XCD
+ * (longest windows first for the tail, contiguous windows per XCD for the
+ * L2; on a community-ordered graph the reference's descending order would
+ * scatter each community over the whole run).  Four small kernels (~30 us)
+ * build the schedule in scratch of about 9 bytes per window taken from the
+ * library's pool and returned to it in stream order on `stream` (the call
+ * does not wait).  Tensors past ~4 GiB take the sequence of the order, as
+ * small graphs do.  Every other path allocates nothing. */
 f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                              float* O, const int32_t* d_window_offsets,
                              const int32_t* d_block_col, const uint16_t* d_tile_mask,
@@ -153,13 +162,13 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
  * reference: for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
  * semantics, kernels and results (bit for bit) as f3s_attention_fwd; the
- * natural-order launch's scratch (heavy-window lists, per-block counts and a
- * bitmap: 0.66 MB) is a fixed device array of the library, one per GPU, held
- * until the process ends.  Limit: W <= 4,194,304 row windows (n <= 67,108,864
- * nodes); larger W returns F3S_EUNSUPPORTED.  Every call on one GPU shares
- * that GPU's array and overwrites it, so calls that overlap in time on one
- * GPU (e.g. on two streams) race; serialise them.  Allocates nothing and
- * never waits for the device. */
+ * schedule's scratch (tables, team list, class counts, one-wave slots and an
+ * order's inverse: 18 MiB) is a fixed device array of the library, one per
+ * GPU, held until the process ends.  Limit: W <= 2,097,152 row windows
+ * (n <= 33,554,432 nodes); larger W returns F3S_EUNSUPPORTED.  Every call on
+ * one GPU shares that GPU's array and overwrites it, so calls that overlap in
+ * time on one GPU (e.g. on two streams) race; serialise them.  Allocates
+ * nothing, clears no memory and never waits for the device. */
 f3s_status f3s_attention_fwd_noalloc(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                                      float* O, const int32_t* d_window_offsets,
                                      const int32_t* d_block_col, const uint16_t* d_tile_mask,

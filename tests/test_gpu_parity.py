@@ -48,7 +48,7 @@ def assert_close(got, want, what=""):
 class Problem:
     """A graph plus fp16 features, on host and device."""
 
-    def __init__(self, f3s, rp, ci, H=1, normal=False, seed=0, Qzero=False):
+    def __init__(self, f3s, rp, ci, H=1, normal=False, seed=0, Qzero=False, f32=False):
         self.f3s = f3s
         self.n = len(rp) - 1
         self.H, self.d = H, 64
@@ -56,6 +56,8 @@ class Problem:
         n = self.n
         r = rng(seed)
         def feat():
+            if f32:   # large inputs: U[-1, 1) drawn in float32
+                return (r.random((n, H, 64), dtype=np.float32) * 2 - 1).astype(np.float16)
             x = r.standard_normal((n, H, 64)) if normal else r.uniform(-1, 1, (n, H, 64))
             return x.astype(np.float16)
         self.Q, self.K, self.V = feat(), feat(), feat()
@@ -532,11 +534,12 @@ def test_concurrent_converter_and_natural_order_launch(gpu):
 
 def test_unplanned_heavy_windows(gpu):
     # Without a plan, windows of more than max(1024, 8 x mean) tiles run as
-    # 16-wave teams in a launch of their own -- given a window order, those
-    # among its first 512 positions; in natural order, the first 512 heavy
-    # windows by index -- and every other window on one wave in a second
-    # launch.  Hubs sit in windows 0, 1 and 562 (1,250 tiles each); the orders
-    # put them first (sorted) or at positions 700, 5 and 100 (one past 512).
+    # 16-wave teams in a launch of their own -- in natural order (the
+    # library's schedule) the first 512 such windows, heaviest first; given a
+    # window order on a launch this size (under 2^18 window-heads), those
+    # among its first 512 entries -- and every other window on one wave.
+    # Hubs sit in windows 0, 1 and 562 (1,250 tiles each); the orders put
+    # them first (sorted) or at positions 700, 5 and 100 (one past 512).
     rp, ci = star_graph(20000, hubs=(0, 3, 17, 9000))
     p = Problem(gpu, rp, ci, H=2, normal=True, seed=61)
     W = p.bsf.W
@@ -562,15 +565,79 @@ def test_unplanned_heavy_windows(gpu):
         assert np.array_equal(got_by["natural"].view(np.uint32), got_by["sorted"].view(np.uint32))
 
 
+def test_unplanned_schedule_names_windows(gpu):
+    # From 2^18 window-heads on, a window order only names the windows to
+    # compute, and the library's schedule runs them: invalid entries are
+    # skipped, a repeated window is computed once, windows the order does
+    # not name are left untouched, and every order gives the bits of a
+    # natural-order call.  4,096 windows x 64 heads; the hub windows 0, 2
+    # and 2,062 (rows of 3,000 random neighbours, over 1,024 tiles) take the
+    # team launch wherever the order puts them.
+    n, H = 65536, 64
+    r = rng(66)
+    rows = [np.arange(n), np.repeat(np.arange(n), 3)]
+    cols = [np.arange(n), r.integers(0, n, 3 * n)]
+    for hub in (0, 40, 33000):
+        rows.append(np.full(3000, hub))
+        cols.append(r.integers(0, n, 3000))
+    key = np.unique(np.concatenate(rows).astype(np.int64) * n + np.concatenate(cols))
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, key // n + 1, 1)
+    rp, ci = np.cumsum(rp).astype(np.int32), (key % n).astype(np.int32)
+    p = Problem(gpu, rp, ci, H=H, seed=64, f32=True)
+    W = p.bsf.W
+    tiles = np.diff(p.bsf.window_offsets.numpy())
+    thr = max(1024, 8 * (-(-int(tiles.sum()) // W)))
+    assert W * H >= 1 << 18 and list(np.nonzero(tiles > thr)[0]) == [0, 2, 2062]
+    r = rng(65)
+    perm = r.permutation(W).astype(np.int32)
+    order = perm.copy()
+    k = np.arange(0, W, 7)
+    order[k] = np.where(k % 3 == 0, -2, np.where(k % 3 == 1, W + 9, order[(k + 1) % W]))
+    named = np.zeros(W, bool)
+    named[order[(order >= 0) & (order < W)]] = True
+    for hub in (0, 2, 2062):     # keep the hub windows named, late in the order
+        if not named[hub]:
+            order[int(np.nonzero(order == -2)[0][-1])] = hub
+            named[hub] = True
+    valid = order[(order >= 0) & (order < W)]
+    assert (~named).any() and len(set(valid.tolist())) < len(valid)     # some repeat
+    rows = np.repeat(named, 16)[:n]
+    # oracle windows: every 61st named window, and the hub windows when masked
+    sample = sorted(set(np.nonzero(named)[0][::61].tolist()) - {0, 2, 2062})
+    dperm, dorder = gpu.DeviceArray.from_numpy(perm), gpu.DeviceArray.from_numpy(order)
+    for masked in (True, False):
+        full = p.run(masked)
+        shuffled = p.run(masked, order=dperm)
+        assert np.array_equal(shuffled.view(np.uint32), full.view(np.uint32)), masked
+        got = p.run(masked, order=dorder)
+        what = f"partial order, scheduled, masked={masked}"
+        assert np.all(np.isnan(got[~rows])), what
+        assert np.array_equal(got[rows].view(np.uint32), full[rows].view(np.uint32)), what
+        # the allocation-free entry point: the order's inverse in its fixed scratch
+        from fused3s_amd import _lib
+        p.dO.fill_bytes(0xFF)
+        bsf = p.bsf
+        assert _lib.hip().f3s_attention_fwd_noalloc(
+            p.dQ.ptr, p.dK.ptr, p.dV.ptr, p.dO.ptr, bsf.window_offsets.ptr, bsf.block_col.ptr,
+            bsf.tile_mask.ptr if masked else None, dorder.ptr, W, n, 64, H, 1.0, None) == 0
+        gpu.synchronize()
+        assert np.array_equal(p.dO.numpy().view(np.uint32), got.view(np.uint32)), what
+        ranges = [(16 * w, 16 * w + 16) for w in (sample + [0, 2, 2062] if masked else sample)]
+        want = p.oracle(masked, rows=ranges)
+        assert_close(np.concatenate([got[a:b] for a, b in ranges]),
+                     np.concatenate([want[r] for r in ranges]), what)
+
+
 def test_unplanned_natural_order_heavy_cap(gpu):
-    # Natural order starts the one-wave launch with the first 4,096 windows
-    # by index of more than max(512, 2 x mean) tiles (and no more than
-    # max(1024, 8 x mean)), the rest following in index order.  Here
-    # 4,200 windows (every 4th of 16,800) hold exactly 600 tiles: the last
-    # 104 are not listed and run in their index position, and the listing
-    # kernels' 256-window blocks each hold 64 of them.  With a window order the rule is max(1024,
-    # 8 x mean) = 1,208 tiles, so no window is heavy there.  Results meet the
-    # oracle; repeated runs give the same bits.
+    # The schedule's classes (natural order): 4,200 windows (every 4th of
+    # 16,800) hold exactly 600 tiles, a class of their own ([512, 1024)
+    # tiles) that the one-wave launch starts first, cut into eight XCD
+    # shares; the threshold for teams, max(1024, 8 x mean) = 1,208 tiles,
+    # takes none of them.  The class spans all 66 of the schedule's
+    # 256-window blocks, 64 windows in each.  The sorted order runs in its
+    # own sequence (no team either).  Results meet the oracle, both orders
+    # give the same bits, and repeated runs too.
     W = 16_800
     n = 16 * W
     heavy_w = np.arange(4200) * 4
@@ -599,6 +666,7 @@ def test_unplanned_natural_order_heavy_cap(gpu):
         assert_close(a, want, f"natural order, 4,200 heavy windows, masked={masked}")
         assert_close(s, want, f"sorted order, masked={masked}")
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert np.array_equal(a.view(np.uint32), s.view(np.uint32))
 
 
 @pytest.mark.parametrize("H", [1, 16])

@@ -1,10 +1,13 @@
 """f3s_attention_fwd_noalloc (the allocation-free variant of the drop-in
-launch, whose natural-order scratch is a fixed device array) against
+launch, whose schedule scratch is a fixed device array) against
 f3s_attention_fwd on the same inputs: bit-identical outputs, both within the
 north-star tolerance of the oracle, over two calls in a row on graphs whose
-heavy windows take the natural-order team launches -- the second graph
-smaller, so stale scratch from the first call would show -- in both
-semantics; and the size limit."""
+heavy windows take the schedule's team launch -- the second graph smaller,
+so stale scratch from the first call would show -- in both semantics, in
+natural order and in an order's sequence; and the size limit.  (The
+scheduled launch with a window order, whose inverse lives in the same
+scratch, is compared in test_gpu_parity.py's
+test_unplanned_schedule_names_windows.)"""
 from __future__ import annotations
 
 import ctypes as C
@@ -34,12 +37,12 @@ def hub_graph(n: int, seed: int, hubs: dict[int, int]) -> tuple[np.ndarray, np.n
     return np.cumsum(rp).astype(np.int32), cc.astype(np.int32)
 
 
-def call(lib_fn, p, masked: bool) -> np.ndarray:
+def call(lib_fn, p, masked: bool, order=None) -> np.ndarray:
     p.dO.fill_bytes(0xFF)   # NaN poison: every row must be written
     bsf = p.bsf
     st = lib_fn(p.dQ.ptr, p.dK.ptr, p.dV.ptr, p.dO.ptr, bsf.window_offsets.ptr,
-                bsf.block_col.ptr, bsf.tile_mask.ptr if masked else None, None, bsf.W, bsf.n,
-                64, p.H, 0.125, None)
+                bsf.block_col.ptr, bsf.tile_mask.ptr if masked else None,
+                order.ptr if order is not None else None, bsf.W, bsf.n, 64, p.H, 0.125, None)
     assert st == 0, lib_fn.__name__
     p.f3s.synchronize()
     return p.dO.numpy()
@@ -49,9 +52,9 @@ def test_noalloc_matches_allocating_entry_point(gpu):
     from fused3s_amd import _lib
     lib = _lib.hip()
     # 40,000 nodes (2,500 windows) then 20,000 (1,250): both above the 512
-    # windows from which natural order lists heavy windows, each with
-    # windows in the large class (more than max(1024, 8 x mean) tiles) and in
-    # the medium one (more than max(512, 2 x mean), at most the large bound)
+    # windows from which the drop-in launch runs its schedule, each with
+    # heavy windows (more than max(1024, 8 x mean) tiles, for the team
+    # launch) and windows of several tile-count classes
     cases = [(40000, 81, {7: 30000, 9000: 30000, 20011: 1000, 33333: 1200, 39999: 800}, 1),
              (20000, 82, {5: 20000, 6000: 900, 11990: 1100}, 2)]
     for n, seed, hubs, H in cases:
@@ -61,25 +64,27 @@ def test_noalloc_matches_allocating_entry_point(gpu):
         W = len(tiles)
         mean = -(-int(tiles.sum()) // W)
         large = max(1024, 8 * mean)
-        medium = max(512, 2 * mean)
-        assert W > 512 and (tiles > large).any() and ((tiles > medium) & (tiles <= large)).any()
+        octaves = set(np.floor(np.log2(tiles[tiles > 0])).astype(int).tolist())
+        assert W > 512 and (tiles > large).any() and len(octaves) >= 4
+        order = gpu.window_order_device(p.bsf)
         for masked in (True, False):
             want = p.oracle(masked, scale=0.125)
-            ref = call(lib.f3s_attention_fwd, p, masked)
-            got = call(lib.f3s_attention_fwd_noalloc, p, masked)
-            what = f"noalloc n={n} H={H} masked={masked}"
-            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), what
-            assert_close(got, want, what)
+            for o in (None, order):
+                ref = call(lib.f3s_attention_fwd, p, masked, o)
+                got = call(lib.f3s_attention_fwd_noalloc, p, masked, o)
+                what = f"noalloc n={n} H={H} masked={masked} ordered={o is not None}"
+                assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), what
+                assert_close(got, want, what)
 
 
 def test_noalloc_rejects_graphs_past_its_scratch(gpu):
     from fused3s_amd import _lib
     lib = _lib.hip()
-    W = (1 << 22) + 1
+    W = (1 << 21) + 1
     dummy = 256   # never dereferenced: the size check comes first
     st = lib.f3s_attention_fwd_noalloc(dummy, dummy, dummy, dummy, dummy, dummy, None, None,
                                        W, 16 * W, 64, 1, 1.0, None)
-    assert st == 5 and b"4194304" in lib.f3s_last_error()
+    assert st == 5 and b"2097152" in lib.f3s_last_error()
 
 
 def test_noalloc_replays_from_a_hip_graph(gpu):
