@@ -478,319 +478,6 @@ hipError_t warm_attention(hipStream_t s)
     return hipGetLastError();
 }
 
-// ----------------------------------------------------------------- planner
-
-// Segment sizes of an automatic plan.  A window is cut into segments only
-// when it is well above the mean window (4x masked, 2x tile-dense: cutting
-// every window of a uniform graph just adds merge traffic) and a large share
-// of one wave slot's part of the pass (5,120 slots; a tenth of it for
-// tile-dense).  seg[0] serves masked passes, seg[1] tile-dense ones.
-__host__ __device__ __forceinline__ void auto_segments(int64_t T, int32_t W, int32_t H,
-                                                       int64_t seg[2])
-{
-    const int64_t mean = W > 0 ? (T + W - 1) / W : 0;
-    int64_t m = 256, dd = 16;
-    if (4 * mean > m) m = 4 * mean;
-    if ((T * H + 8191) / 8192 > m) m = (T * H + 8191) / 8192;
-    if (2 * mean > dd) dd = 2 * mean;
-    if ((T * H + 51199) / 51200 > dd) dd = (T * H + 51199) / 51200;
-    seg[0] = m < INT32_MAX ? m : INT32_MAX;
-    seg[1] = dd < INT32_MAX ? dd : INT32_MAX;
-}
-
-// Work items per order position for one or two item sets: counts[3 k + 0]
-// items, [3 k + 1] partial slots, [3 k + 2] split windows of set k, each
-// [W].  seg_fixed > 0 is the one set's segment size; 0 takes the automatic
-// sizes from T = offs[W] (thread 0 also reports T and the sizes in info).
-__global__ void plan_count(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
-                           int32_t W, int32_t H, int32_t seg_fixed, int32_t nsets, int32_t team0,
-                           int32_t team1, int32_t* __restrict__ counts, int64_t* __restrict__ info)
-{
-    const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
-    const int32_t T = W > 0 ? max(0, offs[W]) : 0;
-    int64_t seg[2];
-    if (seg_fixed > 0) {
-        seg[0] = seg[1] = seg_fixed;
-    } else {
-        auto_segments(T, W, H, seg);
-    }
-    if (L == 0) {
-        info[0] = T;
-        info[1] = seg[0];
-        info[2] = seg[1];
-    }
-    if (L >= W) return;
-    const int32_t w = order ? order[L] : L;
-    int32_t nt = 0;
-    if (w >= 0 && w < W) {
-        const int32_t tb = max(0, min(offs[w], T)), te = max(tb, min(offs[w + 1], T));
-        nt = te - tb;
-    }
-    for (int k = 0; k < nsets; ++k) {
-        const int32_t team = k == 0 ? team0 : team1;
-        int32_t ns = 1;
-        if (team > 1) {
-            ns = team;   // a team's items, merged in LDS: no partials
-        } else if (nt > seg[k]) {
-            ns = (int32_t)((nt + seg[k] - 1) / seg[k]);
-        }
-        const bool split = team == 1 && ns > 1;
-        counts[(3 * k + 0) * (int64_t)W + L] = ns;
-        counts[(3 * k + 1) * (int64_t)W + L] = split ? ns : 0;
-        counts[(3 * k + 2) * (int64_t)W + L] = split ? 1 : 0;
-    }
-}
-
-// info[3 + j] = total of scanned count array j (bases[j][W]).
-__global__ void plan_totals(const int64_t* __restrict__ bases, int32_t W, int32_t arrays,
-                            int64_t* __restrict__ info)
-{
-    const int j = threadIdx.x;
-    if (j < arrays) info[3 + j] = bases[(int64_t)j * ((int64_t)W + 1) + W];
-}
-
-__global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
-                          int32_t W, int32_t seg, int32_t team,
-                          const int64_t* __restrict__ item_base,
-                          const int64_t* __restrict__ slot_base,
-                          const int64_t* __restrict__ split_base, Item* __restrict__ items,
-                          SplitInfo* __restrict__ splits)
-{
-    const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
-    if (L >= W) return;
-    const int32_t w = order ? order[L] : L;
-    const int64_t ib = item_base[L];
-    const int32_t ns = (int32_t)(item_base[L + 1] - ib);
-    if (w < 0 || w >= W) {
-        for (int32_t k = 0; k < ns; ++k)
-            items[ib + k] = Item{-1, 0, 0, -1};   // no window: the pass skips these
-        return;
-    }
-    const int32_t T = offs[W];
-    const int32_t tb = max(0, min(offs[w], T)), te = max(tb, min(offs[w + 1], T));
-    if (team > 1) {
-        for (int32_t k = 0; k < team; ++k)
-            items[ib + k] = Item{w, team_part(tb, te, k, team), team_part(tb, te, k + 1, team), -1};
-        return;
-    }
-    if (ns == 1) {
-        items[ib] = Item{w, tb, te, -1};
-        return;
-    }
-    const int32_t sb = (int32_t)slot_base[L];
-    splits[split_base[L]] = SplitInfo{w, sb, ns, 0};
-    for (int32_t k = 0; k < ns; ++k) {
-        const int32_t a = tb + k * seg;
-        items[ib + k] = Item{w, a, min(te, a + seg), sb + k};
-    }
-}
-
-__global__ void offsets_to_i32_plan(const int64_t* __restrict__ in, int32_t* __restrict__ out,
-                                    int64_t count)
-{
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < count) out[i] = (int32_t)in[i];
-}
-
-// Attended columns of each planned item (masked semantics): one wave per
-// item counts them (pass 1) or lists them, in tile order, padded to whole
-// chunks (pass 2) -- the expansion the ring path performs on every pass,
-// done once per graph.
-template <bool FILL>
-__global__ void __launch_bounds__(256)
-plan_columns(const Item* __restrict__ items, int64_t num_items,
-             const int32_t* __restrict__ block_col, const uint16_t* __restrict__ tile_mask,
-             int32_t n, uint32_t ref_stride, uint32_t no_ref, int32_t* __restrict__ nchunks,
-             const int64_t* __restrict__ chunk_base, uint32_t* __restrict__ columns)
-{
-    const int64_t it = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
-    const int lane = threadIdx.x % kWave;
-    if (it >= num_items) return;
-    const Item item = items[it];
-    const int32_t nbc = (n + 15) >> 4;
-    int64_t pos = 0;   // wave-uniform
-    uint32_t* rec0 = FILL ? columns + chunk_base[it] * 64 : nullptr;
-    for (int32_t t0 = item.tb; t0 < item.te; t0 += kWave) {
-        const int32_t t = t0 + lane;
-        uint32_t u = 0;
-        int32_t bc = 0;
-        uint32_t wd[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (t < item.te) {
-            bc = block_col[t];
-            if ((uint32_t)bc < (uint32_t)nbc) {
-                const int32_t left = n - bc * 16;
-                const uint32_t vmask = left >= 16 ? 0xffffu : ((1u << left) - 1u);
-                const uint4* mp = reinterpret_cast<const uint4*>(tile_mask + (int64_t)t * 16);
-                const uint4 a = mp[0], b = mp[1];
-                wd[0] = a.x; wd[1] = a.y; wd[2] = a.z; wd[3] = a.w;
-                wd[4] = b.x; wd[5] = b.y; wd[6] = b.z; wd[7] = b.w;
-                const uint32_t o = a.x | a.y | a.z | a.w | b.x | b.y | b.z | b.w;
-                u = (o | (o >> 16)) & vmask;
-            }
-        }
-        const int occ = __popc(u);
-        const int incl = wave_scan_incl(occ);
-        if (FILL && occ) {
-            int64_t q = pos + incl - occ;
-            const uint32_t base = (uint32_t)bc * 16 * ref_stride;
-            uint32_t rest = u;
-            while (rest) {
-                const int c = __ffs(rest) - 1;
-                rest &= rest - 1;
-                uint32_t* rec = rec0 + (q >> 5) * 64;
-                rec[q & 31] = base + (uint32_t)c * ref_stride;
-                rec[32 + (q & 31)] = column_rows(wd, c);
-                ++q;
-            }
-        }
-        pos += __builtin_amdgcn_readlane(incl, kWave - 1);
-    }
-    const int64_t nch = (pos + kChunk - 1) / kChunk;
-    if (!FILL) {
-        if (lane == 0) nchunks[it] = (int32_t)nch;
-        return;
-    }
-    // pad the last chunk with slots no row attends, read as zero
-    for (int64_t q = pos + lane; q < nch * kChunk; q += kWave) {
-        uint32_t* rec = rec0 + (q >> 5) * 64;
-        rec[q & 31] = no_ref;
-        rec[32 + (q & 31)] = 0u;
-    }
-}
-
-}  // namespace f3s
-
-namespace f3s {
-
-// Lays out a plan's work items: counts for every item set in one pass, one
-// host round trip for their totals (and, for automatic plans, T and the
-// segment sizes computed on the device), then the item lists; the partial
-// buffer is shared by the sets (a plan serves one pass at a time).
-static f3s_status build_plan_sets(f3s_plan* p, const int32_t* d_window_offsets,
-                                  const int32_t* d_window_order, int32_t seg_tiles,
-                                  hipStream_t st)
-{
-    const int32_t W = p->W, H = p->H;
-    const bool automatic = seg_tiles == 0;
-    const int32_t team_m = automatic ? team_for(W, H, true) : 1;
-    const int32_t team_d = automatic ? team_for(W, H, false) : 1;
-    const int32_t nsets = automatic ? 2 : 1;
-    const int arrays = 3 * nsets;
-    const size_t cnt_bytes = sizeof(int32_t) * (size_t)arrays * (size_t)W;
-    const size_t base_bytes = sizeof(int64_t) * (size_t)arrays * ((size_t)W + 1);
-    const size_t tmp_bytes = sizeof(int64_t) * (size_t)scan_tmp_elems(W);
-    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    StreamBuffer buf(st);
-    F3S_TRY(buf.reserve(256 + al(cnt_bytes) + al(base_bytes) + al(tmp_bytes)));
-    char* q = static_cast<char*>(buf.ptr);
-    int64_t* info = reinterpret_cast<int64_t*>(q);           // [0] T, [1..2] segs, [3..] totals
-    int32_t* counts = reinterpret_cast<int32_t*>(q + 256);
-    int64_t* bases = reinterpret_cast<int64_t*>(q + 256 + al(cnt_bytes));
-    int64_t* tmp = reinterpret_cast<int64_t*>(q + 256 + al(cnt_bytes) + al(base_bytes));
-    hipLaunchKernelGGL(plan_count, dim3((unsigned)ceil_div(W > 0 ? W : 1, 256)), dim3(256), 0, st,
-                       d_window_offsets, d_window_order, W, H, seg_tiles, nsets, team_m, team_d,
-                       counts, info);
-    F3S_HIP(hipGetLastError());
-    for (int j = 0; j < arrays; ++j)
-        F3S_TRY(exclusive_scan_i32_to_i64(counts + (size_t)j * W, bases + (size_t)j * (W + 1), W,
-                                          tmp, st));
-    hipLaunchKernelGGL(plan_totals, dim3(1), dim3(64), 0, st, bases, W, arrays, info);
-    F3S_HIP(hipGetLastError());
-    int64_t* h = host_staging();
-    F3S_HIP(hipMemcpyAsync(h, info, sizeof(int64_t) * (3 + arrays), hipMemcpyDeviceToHost, st));
-    F3S_HIP(hipStreamSynchronize(st));
-    p->T = h[0];
-    const int32_t seg_m = (int32_t)h[1], seg_d = (int32_t)h[2];
-    p->has_dense = automatic && (team_d != team_m || (team_d == 1 && seg_d != seg_m));
-    int64_t max_slots = 0;
-    for (int k = 0; k < nsets; ++k) {
-        f3s_item_set& set = k == 0 ? p->masked : p->dense;
-        if (k == 1 && !p->has_dense) break;
-        set.seg = k == 0 ? seg_m : seg_d;
-        set.team = k == 0 ? team_m : team_d;
-        set.num_items = h[3 + 3 * k];
-        set.num_slots = h[3 + 3 * k + 1];
-        set.num_split = h[3 + 3 * k + 2];
-        if (set.num_slots > max_slots) max_slots = set.num_slots;
-        F3S_TRY(set.items.reserve(sizeof(Item) * (size_t)(set.num_items + 1), st));
-        F3S_TRY(set.splits.reserve(sizeof(SplitInfo) * (size_t)(set.num_split + 1), st));
-    }
-    F3S_TRY(p->partials.reserve(sizeof(float) * (size_t)kPartialFloats * H * (size_t)(max_slots + 1),
-                                st));
-    for (int k = 0; k < nsets && W > 0; ++k) {
-        if (k == 1 && !p->has_dense) break;
-        f3s_item_set& set = k == 0 ? p->masked : p->dense;
-        const int64_t* bk = bases + (size_t)3 * k * (W + 1);
-        hipLaunchKernelGGL(plan_fill, dim3((unsigned)ceil_div(W, 256)), dim3(256), 0, st,
-                           d_window_offsets, d_window_order, W, set.seg, set.team, bk,
-                           bk + (W + 1), bk + 2 * (size_t)(W + 1),
-                           reinterpret_cast<Item*>(set.items.ptr),
-                           reinterpret_cast<SplitInfo*>(set.splits.ptr));
-        F3S_HIP(hipGetLastError());
-    }
-    // the plan is complete (and its memory usable on any stream) on return
-    F3S_HIP(hipStreamSynchronize(st));
-    return F3S_OK;
-}
-
-static f3s_status check_attention_args(const void* Q, const void* K, const void* V, const void* O,
-                                       int32_t n, int32_t d, int32_t H)
-{
-    F3S_REQUIRE(n >= 0, "attention: negative n");
-    if (d != kD) {
-        set_error("attention: only d == 64 is implemented (FEAT_DIM_FIXED of the reference)");
-        return F3S_EUNSUPPORTED;
-    }
-    if (H < 1 || H > kMaxHeads) {
-        set_error("attention: H must be in [1, 64]");
-        return F3S_EUNSUPPORTED;
-    }
-    F3S_REQUIRE(n == 0 || (Q && K && V && O), "attention: NULL feature pointer");
-    F3S_REQUIRE(((((uintptr_t)Q) | ((uintptr_t)K) | ((uintptr_t)V) | ((uintptr_t)O)) & 15) == 0,
-                "attention: Q, K, V, O must be 16-byte aligned");
-    return F3S_OK;
-}
-
-template <int MODE, bool WIDE>
-static void launch_mw(const AttnParams& p, int64_t waves, hipStream_t st)
-{
-    if constexpr (!WIDE) {
-        // teams (small graphs; never wide): one workgroup per (window, head)
-        if (p.team == kTeamLarge) {
-            hipLaunchKernelGGL((fused_attention_kernel<MODE, kTeamLarge, false, kTeamLarge>),
-                               dim3((unsigned)(waves / kTeamLarge)), dim3(kTeamLarge * kWave), 0,
-                               st, p);
-            return;
-        }
-        if (p.team == kTeamSmall) {
-            hipLaunchKernelGGL((fused_attention_kernel<MODE, kTeamSmall, false, kTeamSmall>),
-                               dim3((unsigned)(waves / kTeamSmall)), dim3(kTeamSmall * kWave), 0,
-                               st, p);
-            return;
-        }
-    }
-    // Small launches use one-wave workgroups so they spread over all CUs.
-    if (waves < 4 * 256 * 2) {
-        hipLaunchKernelGGL((fused_attention_kernel<MODE, 1, WIDE, 1>), dim3((unsigned)waves),
-                           dim3(kWave), 0, st, p);
-    } else {
-        hipLaunchKernelGGL((fused_attention_kernel<MODE, 4, WIDE, 1>),
-                           dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
-    }
-    if (p.num_split > 0)
-        hipLaunchKernelGGL(merge_partials_kernel,
-                           dim3((unsigned)ceil_div(p.num_split * p.H, 4)), dim3(256), 0, st, p);
-}
-
-template <int MODE>
-static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
-{
-    if (wide_features(p.n, p.H))
-        launch_mw<MODE, true>(p, waves, st);
-    else
-        launch_mw<MODE, false>(p, waves, st);
-}
-
 // ---------------------------------------------------------------------------
 // Schedule of the unplanned launch on graphs of more than kHeavyMaxWindows
 // windows, in natural order and, from kSchedOrderedMin window-heads on, with
@@ -904,7 +591,7 @@ constexpr int kSegRegs = 32;
 static_assert(kSchedClasses * kScanSegs == 1024, "one lane per (class, segment)");
 static_assert(kSchedClasses == kWave, "one lane per class in the table scans");
 __global__ void __launch_bounds__(1024)
-sched_scan(int32_t* __restrict__ counts, int32_t nb, SchedTables* __restrict__ tab)
+sched_scan(int32_t* __restrict__ counts, int32_t nb, int32_t team_cap, SchedTables* __restrict__ tab)
 {
     __shared__ int32_t total[kSchedClasses];
     __shared__ int32_t size[kSchedClasses];
@@ -956,13 +643,13 @@ sched_scan(int32_t* __restrict__ counts, int32_t nb, SchedTables* __restrict__ t
     __syncthreads();
     if (wid == 0) {
         // lane = class: the heavy classes come first, and the team list takes
-        // their first kHeavyMaxWindows windows
+        // their first team_cap windows
         const int32_t tot = total[lane];
         const int32_t heavy = lane < kSchedClasses / 2 ? tot : 0;
         const int32_t before = wave_inclusive_scan(heavy) - heavy;
-        const int32_t take = max(0, min(heavy, kHeavyMaxWindows - before));
-        const int32_t team_all = min(kHeavyMaxWindows, __shfl(before + heavy, kWave - 1));
-        tab->team_base[lane] = lane < kSchedClasses / 2 ? min(before, kHeavyMaxWindows) : team_all;
+        const int32_t take = max(0, min(heavy, team_cap - before));
+        const int32_t team_all = min(team_cap, __shfl(before + heavy, kWave - 1));
+        tab->team_base[lane] = lane < kSchedClasses / 2 ? min(before, team_cap) : team_all;
         tab->taken[lane] = take;
         tab->size[lane] = size[lane] = tot - take;
         if (lane == 0) tab->team_items = team_all;
@@ -1022,6 +709,398 @@ sched_fill(const int32_t* __restrict__ window_offsets, const int32_t* __restrict
     sched[x * L + tab->xcd_base[x][q] + (r2 - sz * x / kXcds)] = w;
 }
 
+// Scratch of the scheduled launch for W windows, in 256-byte sections: the
+// tables, the team list, the class counts (kSchedClasses per block of
+// kSchedBlock windows), the one-wave slots and, given a window order, its
+// inverse.
+struct SchedScratch {
+    size_t tab, team, counts, sched, inv, bytes;
+};
+constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+constexpr SchedScratch sched_scratch(int64_t W, bool ordered)
+{
+    auto up = round256;
+    SchedScratch l{};
+    l.tab = 0;
+    l.team = up(sizeof(SchedTables));
+    l.counts = l.team + up(sizeof(int32_t) * kHeavyMaxWindows);
+    l.sched = l.counts + up(sizeof(int32_t) * kSchedClasses * (size_t)ceil_div(W, kSchedBlock));
+    l.inv = l.sched + up(sizeof(int32_t) * kXcds * (size_t)sched_xcd_slots(W));
+    l.bytes = l.inv + (ordered ? up(sizeof(int32_t) * (size_t)W) : 0);
+    return l;
+}
+
+// Builds the schedule of W windows (those `order` names, or all) into scratch
+// `sp` laid out by sched_scratch(W, order != NULL): a team list of at most
+// team_cap heavy windows (kHeavyMaxWindows entries, -1 past its end) and
+// kXcds * L one-wave slots (-1 where empty), L = sched_xcd_slots(W).
+static f3s_status launch_schedule(const int32_t* d_window_offsets, const int32_t* d_window_order,
+                                  int32_t W, int32_t team_cap, char* sp, hipStream_t st,
+                                  int32_t** team_out, int32_t** sched_out)
+{
+    const bool ordered = d_window_order != nullptr;
+    const SchedScratch lay = sched_scratch(W, ordered);
+    SchedTables* tab = reinterpret_cast<SchedTables*>(sp + lay.tab);
+    int32_t* team = reinterpret_cast<int32_t*>(sp + lay.team);
+    int32_t* counts = reinterpret_cast<int32_t*>(sp + lay.counts);
+    int32_t* sched = reinterpret_cast<int32_t*>(sp + lay.sched);
+    int32_t* inv = ordered ? reinterpret_cast<int32_t*>(sp + lay.inv) : nullptr;
+    const int32_t nb = (int32_t)ceil_div(W, kSchedBlock);
+    const int64_t L = sched_xcd_slots(W);
+    const int32_t fill_blocks = (int32_t)std::max<int64_t>(nb, ceil_div(kXcds * L, kSchedBlock));
+    if (ordered)
+        hipLaunchKernelGGL(sched_inverse, dim3((unsigned)nb), dim3(kSchedBlock), 0, st,
+                           d_window_order, W, inv);
+    hipLaunchKernelGGL(sched_count, dim3((unsigned)nb), dim3(kSchedBlock), 0, st,
+                       d_window_offsets, d_window_order, inv, W, nb, counts);
+    hipLaunchKernelGGL(sched_scan, dim3(1), dim3(1024), 0, st, counts, nb, team_cap, tab);
+    hipLaunchKernelGGL(sched_fill, dim3((unsigned)fill_blocks), dim3(kSchedBlock), 0, st,
+                       d_window_offsets, d_window_order, inv, W, nb, counts, tab, (int32_t)L,
+                       team, sched);
+    const hipError_t le = hipGetLastError();
+    if (le != hipSuccess) return hip_fail(le, "window schedule", __FILE__, __LINE__);
+    *team_out = team;
+    *sched_out = sched;
+    return F3S_OK;
+}
+
+// ----------------------------------------------------------------- planner
+
+// Segment sizes of an automatic plan.  A window is cut into segments only
+// when it is well above the mean window (4x masked, 2x tile-dense: cutting
+// every window of a uniform graph just adds merge traffic) and a large share
+// of one wave slot's part of the pass (5,120 slots; a tenth of it for
+// tile-dense).  seg[0] serves masked passes, seg[1] tile-dense ones.
+__host__ __device__ __forceinline__ void auto_segments(int64_t T, int32_t W, int32_t H,
+                                                       int64_t seg[2])
+{
+    const int64_t mean = W > 0 ? (T + W - 1) / W : 0;
+    int64_t m = 256, dd = 16;
+    if (4 * mean > m) m = 4 * mean;
+    if ((T * H + 8191) / 8192 > m) m = (T * H + 8191) / 8192;
+    if (2 * mean > dd) dd = 2 * mean;
+    if ((T * H + 51199) / 51200 > dd) dd = (T * H + 51199) / 51200;
+    seg[0] = m < INT32_MAX ? m : INT32_MAX;
+    seg[1] = dd < INT32_MAX ? dd : INT32_MAX;
+}
+
+// Work items per position of the plan's sequence (P positions; window
+// order[L], or L; invalid entries hold no window) for one or two item sets:
+// counts[3 k + 0] items, [3 k + 1] partial slots, [3 k + 2] split windows of
+// set k, each [P].  seg_fixed > 0 is the one set's segment size; 0 takes the
+// automatic sizes from T = offs[W] (thread 0 also reports T and the sizes in
+// info).
+__global__ void plan_count(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
+                           int32_t W, int32_t P, int32_t H, int32_t seg_fixed, int32_t nsets,
+                           int32_t team0, int32_t team1, int32_t* __restrict__ counts,
+                           int64_t* __restrict__ info)
+{
+    const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
+    const int32_t T = W > 0 ? max(0, offs[W]) : 0;
+    int64_t seg[2];
+    if (seg_fixed > 0) {
+        seg[0] = seg[1] = seg_fixed;
+    } else {
+        auto_segments(T, W, H, seg);
+    }
+    if (L == 0) {
+        info[0] = T;
+        info[1] = seg[0];
+        info[2] = seg[1];
+    }
+    if (L >= P) return;
+    const int32_t w = order ? order[L] : L;
+    int32_t nt = 0;
+    if (w >= 0 && w < W) {
+        const int32_t tb = max(0, min(offs[w], T)), te = max(tb, min(offs[w + 1], T));
+        nt = te - tb;
+    }
+    for (int k = 0; k < nsets; ++k) {
+        const int32_t team = k == 0 ? team0 : team1;
+        int32_t ns = 1;
+        if (team > 1) {
+            ns = team;   // a team's items, merged in LDS: no partials
+        } else if (nt > seg[k]) {
+            ns = (int32_t)((nt + seg[k] - 1) / seg[k]);
+        }
+        const bool split = team == 1 && ns > 1;
+        counts[(3 * k + 0) * (int64_t)P + L] = ns;
+        counts[(3 * k + 1) * (int64_t)P + L] = split ? ns : 0;
+        counts[(3 * k + 2) * (int64_t)P + L] = split ? 1 : 0;
+    }
+}
+
+// info[3 + j] = total of scanned count array j (bases[j][P]).
+__global__ void plan_totals(const int64_t* __restrict__ bases, int32_t P, int32_t arrays,
+                            int64_t* __restrict__ info)
+{
+    const int j = threadIdx.x;
+    if (j < arrays) info[3 + j] = bases[(int64_t)j * ((int64_t)P + 1) + P];
+}
+
+__global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __restrict__ order,
+                          int32_t W, int32_t P, int32_t seg, int32_t team,
+                          const int64_t* __restrict__ item_base,
+                          const int64_t* __restrict__ slot_base,
+                          const int64_t* __restrict__ split_base, Item* __restrict__ items,
+                          SplitInfo* __restrict__ splits)
+{
+    const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
+    if (L >= P) return;
+    const int32_t w = order ? order[L] : L;
+    const int64_t ib = item_base[L];
+    const int32_t ns = (int32_t)(item_base[L + 1] - ib);
+    if (w < 0 || w >= W) {
+        for (int32_t k = 0; k < ns; ++k)
+            items[ib + k] = Item{-1, 0, 0, -1};   // no window: the pass skips these
+        return;
+    }
+    const int32_t T = offs[W];
+    const int32_t tb = max(0, min(offs[w], T)), te = max(tb, min(offs[w + 1], T));
+    if (team > 1) {
+        for (int32_t k = 0; k < team; ++k)
+            items[ib + k] = Item{w, team_part(tb, te, k, team), team_part(tb, te, k + 1, team), -1};
+        return;
+    }
+    if (ns == 1) {
+        items[ib] = Item{w, tb, te, -1};
+        return;
+    }
+    const int32_t sb = (int32_t)slot_base[L];
+    splits[split_base[L]] = SplitInfo{w, sb, ns, 0};
+    for (int32_t k = 0; k < ns; ++k) {
+        const int32_t a = tb + k * seg;
+        items[ib + k] = Item{w, a, min(te, a + seg), sb + k};
+    }
+}
+
+__global__ void offsets_to_i32_plan(const int64_t* __restrict__ in, int32_t* __restrict__ out,
+                                    int64_t count)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) out[i] = (int32_t)in[i];
+}
+
+// Attended columns of each planned item (masked semantics): one wave per
+// item counts them (pass 1) or lists them, in tile order, padded to whole
+// chunks (pass 2) -- the expansion the ring path performs on every pass,
+// done once per graph.
+template <bool FILL>
+__global__ void __launch_bounds__(256)
+plan_columns(const Item* __restrict__ items, int64_t num_items,
+             const int32_t* __restrict__ block_col, const uint16_t* __restrict__ tile_mask,
+             int32_t n, uint32_t ref_stride, uint32_t no_ref, int32_t* __restrict__ nchunks,
+             const int64_t* __restrict__ chunk_base, uint32_t* __restrict__ columns)
+{
+    const int64_t it = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (it >= num_items) return;
+    const Item item = items[it];
+    const int32_t nbc = (n + 15) >> 4;
+    int64_t pos = 0;   // wave-uniform
+    uint32_t* rec0 = FILL ? columns + chunk_base[it] * 64 : nullptr;
+    for (int32_t t0 = item.tb; t0 < item.te; t0 += kWave) {
+        const int32_t t = t0 + lane;
+        uint32_t u = 0;
+        int32_t bc = 0;
+        uint32_t wd[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (t < item.te) {
+            bc = block_col[t];
+            if ((uint32_t)bc < (uint32_t)nbc) {
+                const int32_t left = n - bc * 16;
+                const uint32_t vmask = left >= 16 ? 0xffffu : ((1u << left) - 1u);
+                const uint4* mp = reinterpret_cast<const uint4*>(tile_mask + (int64_t)t * 16);
+                const uint4 a = mp[0], b = mp[1];
+                wd[0] = a.x; wd[1] = a.y; wd[2] = a.z; wd[3] = a.w;
+                wd[4] = b.x; wd[5] = b.y; wd[6] = b.z; wd[7] = b.w;
+                const uint32_t o = a.x | a.y | a.z | a.w | b.x | b.y | b.z | b.w;
+                u = (o | (o >> 16)) & vmask;
+            }
+        }
+        const int occ = __popc(u);
+        const int incl = wave_scan_incl(occ);
+        if (FILL && occ) {
+            int64_t q = pos + incl - occ;
+            const uint32_t base = (uint32_t)bc * 16 * ref_stride;
+            uint32_t rest = u;
+            while (rest) {
+                const int c = __ffs(rest) - 1;
+                rest &= rest - 1;
+                uint32_t* rec = rec0 + (q >> 5) * 64;
+                rec[q & 31] = base + (uint32_t)c * ref_stride;
+                rec[32 + (q & 31)] = column_rows(wd, c);
+                ++q;
+            }
+        }
+        pos += __builtin_amdgcn_readlane(incl, kWave - 1);
+    }
+    const int64_t nch = (pos + kChunk - 1) / kChunk;
+    if (!FILL) {
+        if (lane == 0) nchunks[it] = (int32_t)nch;
+        return;
+    }
+    // pad the last chunk with slots no row attends, read as zero
+    for (int64_t q = pos + lane; q < nch * kChunk; q += kWave) {
+        uint32_t* rec = rec0 + (q >> 5) * 64;
+        rec[q & 31] = no_ref;
+        rec[32 + (q & 31)] = 0u;
+    }
+}
+
+}  // namespace f3s
+
+namespace f3s {
+
+// Lays out a plan's work items: counts for every item set in one pass, one
+// host round trip for their totals (and, for automatic plans, T and the
+// segment sizes computed on the device), then the item lists; the partial
+// buffer is shared by the sets (a plan serves one pass at a time).  From
+// kSchedOrderedMin window-heads on, with one wave per item (no teams), the
+// items follow the drop-in launch's schedule (classes of tile count,
+// heaviest first, eight contiguous XCD shares; no team list: heavy windows
+// are split into segments) and the pass maps them XCD-contiguously, whatever
+// the window order; otherwise they follow the order's sequence.  (On config
+// 4, 62,500 window-heads, the schedule's layout measured 9 % slower than the
+// descending order's sequence: 597 against 548 us per planned pass.)
+static f3s_status build_plan_sets(f3s_plan* p, const int32_t* d_window_offsets,
+                                  const int32_t* d_window_order, int32_t seg_tiles,
+                                  hipStream_t st)
+{
+    const int32_t W = p->W, H = p->H;
+    const bool automatic = seg_tiles == 0;
+    const int32_t team_m = automatic ? team_for(W, H, true) : 1;
+    const int32_t team_d = automatic ? team_for(W, H, false) : 1;
+    const int32_t nsets = automatic ? 2 : 1;
+    const int arrays = 3 * nsets;
+    const bool scheduled = W > kHeavyMaxWindows && team_m == 1 && team_d == 1 &&
+                           (int64_t)W * H >= kSchedOrderedMin;
+    StreamBuffer sbuf(st);
+    const int32_t* seq = d_window_order;   // the sequence of positions
+    int32_t P = W;
+    if (scheduled) {
+        F3S_TRY(sbuf.reserve(sched_scratch(W, d_window_order != nullptr).bytes));
+        int32_t* team = nullptr;
+        int32_t* sched = nullptr;
+        F3S_TRY(launch_schedule(d_window_offsets, d_window_order, W, 0,
+                                static_cast<char*>(sbuf.ptr), st, &team, &sched));
+        seq = sched;
+        P = (int32_t)(kXcds * sched_xcd_slots(W));
+    }
+    p->xcd_contiguous = scheduled || d_window_order == nullptr;
+    const size_t cnt_bytes = sizeof(int32_t) * (size_t)arrays * (size_t)P;
+    const size_t base_bytes = sizeof(int64_t) * (size_t)arrays * ((size_t)P + 1);
+    const size_t tmp_bytes = sizeof(int64_t) * (size_t)scan_tmp_elems(P);
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    StreamBuffer buf(st);
+    F3S_TRY(buf.reserve(256 + al(cnt_bytes) + al(base_bytes) + al(tmp_bytes)));
+    char* q = static_cast<char*>(buf.ptr);
+    int64_t* info = reinterpret_cast<int64_t*>(q);           // [0] T, [1..2] segs, [3..] totals
+    int32_t* counts = reinterpret_cast<int32_t*>(q + 256);
+    int64_t* bases = reinterpret_cast<int64_t*>(q + 256 + al(cnt_bytes));
+    int64_t* tmp = reinterpret_cast<int64_t*>(q + 256 + al(cnt_bytes) + al(base_bytes));
+    hipLaunchKernelGGL(plan_count, dim3((unsigned)ceil_div(P > 0 ? P : 1, 256)), dim3(256), 0, st,
+                       d_window_offsets, seq, W, P, H, seg_tiles, nsets, team_m, team_d, counts,
+                       info);
+    F3S_HIP(hipGetLastError());
+    for (int j = 0; j < arrays; ++j)
+        F3S_TRY(exclusive_scan_i32_to_i64(counts + (size_t)j * P, bases + (size_t)j * (P + 1), P,
+                                          tmp, st));
+    hipLaunchKernelGGL(plan_totals, dim3(1), dim3(64), 0, st, bases, P, arrays, info);
+    F3S_HIP(hipGetLastError());
+    int64_t* h = host_staging();
+    F3S_HIP(hipMemcpyAsync(h, info, sizeof(int64_t) * (3 + arrays), hipMemcpyDeviceToHost, st));
+    F3S_HIP(hipStreamSynchronize(st));
+    p->T = h[0];
+    const int32_t seg_m = (int32_t)h[1], seg_d = (int32_t)h[2];
+    p->has_dense = automatic && (team_d != team_m || (team_d == 1 && seg_d != seg_m));
+    int64_t max_slots = 0;
+    for (int k = 0; k < nsets; ++k) {
+        f3s_item_set& set = k == 0 ? p->masked : p->dense;
+        if (k == 1 && !p->has_dense) break;
+        set.seg = k == 0 ? seg_m : seg_d;
+        set.team = k == 0 ? team_m : team_d;
+        set.num_items = h[3 + 3 * k];
+        set.num_slots = h[3 + 3 * k + 1];
+        set.num_split = h[3 + 3 * k + 2];
+        if (set.num_slots > max_slots) max_slots = set.num_slots;
+        F3S_TRY(set.items.reserve(sizeof(Item) * (size_t)(set.num_items + 1), st));
+        F3S_TRY(set.splits.reserve(sizeof(SplitInfo) * (size_t)(set.num_split + 1), st));
+    }
+    F3S_TRY(p->partials.reserve(sizeof(float) * (size_t)kPartialFloats * H * (size_t)(max_slots + 1),
+                                st));
+    for (int k = 0; k < nsets && P > 0; ++k) {
+        if (k == 1 && !p->has_dense) break;
+        f3s_item_set& set = k == 0 ? p->masked : p->dense;
+        const int64_t* bk = bases + (size_t)3 * k * (P + 1);
+        hipLaunchKernelGGL(plan_fill, dim3((unsigned)ceil_div(P, 256)), dim3(256), 0, st,
+                           d_window_offsets, seq, W, P, set.seg, set.team, bk, bk + (P + 1),
+                           bk + 2 * (size_t)(P + 1), reinterpret_cast<Item*>(set.items.ptr),
+                           reinterpret_cast<SplitInfo*>(set.splits.ptr));
+        F3S_HIP(hipGetLastError());
+    }
+    // the plan is complete (and its memory usable on any stream) on return
+    F3S_HIP(hipStreamSynchronize(st));
+    return F3S_OK;
+}
+
+static f3s_status check_attention_args(const void* Q, const void* K, const void* V, const void* O,
+                                       int32_t n, int32_t d, int32_t H)
+{
+    F3S_REQUIRE(n >= 0, "attention: negative n");
+    if (d != kD) {
+        set_error("attention: only d == 64 is implemented (FEAT_DIM_FIXED of the reference)");
+        return F3S_EUNSUPPORTED;
+    }
+    if (H < 1 || H > kMaxHeads) {
+        set_error("attention: H must be in [1, 64]");
+        return F3S_EUNSUPPORTED;
+    }
+    F3S_REQUIRE(n == 0 || (Q && K && V && O), "attention: NULL feature pointer");
+    F3S_REQUIRE(((((uintptr_t)Q) | ((uintptr_t)K) | ((uintptr_t)V) | ((uintptr_t)O)) & 15) == 0,
+                "attention: Q, K, V, O must be 16-byte aligned");
+    return F3S_OK;
+}
+
+template <int MODE, bool WIDE>
+static void launch_mw(const AttnParams& p, int64_t waves, hipStream_t st)
+{
+    if constexpr (!WIDE) {
+        // teams (small graphs; never wide): one workgroup per (window, head)
+        if (p.team == kTeamLarge) {
+            hipLaunchKernelGGL((fused_attention_kernel<MODE, kTeamLarge, false, kTeamLarge>),
+                               dim3((unsigned)(waves / kTeamLarge)), dim3(kTeamLarge * kWave), 0,
+                               st, p);
+            return;
+        }
+        if (p.team == kTeamSmall) {
+            hipLaunchKernelGGL((fused_attention_kernel<MODE, kTeamSmall, false, kTeamSmall>),
+                               dim3((unsigned)(waves / kTeamSmall)), dim3(kTeamSmall * kWave), 0,
+                               st, p);
+            return;
+        }
+    }
+    // Small launches use one-wave workgroups so they spread over all CUs.
+    if (waves < 4 * 256 * 2) {
+        hipLaunchKernelGGL((fused_attention_kernel<MODE, 1, WIDE, 1>), dim3((unsigned)waves),
+                           dim3(kWave), 0, st, p);
+    } else {
+        hipLaunchKernelGGL((fused_attention_kernel<MODE, 4, WIDE, 1>),
+                           dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
+    }
+    if (p.num_split > 0)
+        hipLaunchKernelGGL(merge_partials_kernel,
+                           dim3((unsigned)ceil_div(p.num_split * p.H, 4)), dim3(256), 0, st, p);
+}
+
+template <int MODE>
+static void launch_m(const AttnParams& p, int64_t waves, hipStream_t st)
+{
+    if (wide_features(p.n, p.H))
+        launch_mw<MODE, true>(p, waves, st);
+    else
+        launch_mw<MODE, false>(p, waves, st);
+}
+
 static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
 {
     if (p.num_items <= 0) return F3S_OK;
@@ -1045,27 +1124,6 @@ static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
         launch_m<kModeRing>(p, waves, st);
     F3S_HIP(hipGetLastError());
     return F3S_OK;
-}
-
-// Scratch of the scheduled launch for W windows, in 256-byte sections: the
-// tables, the team list, the class counts (kSchedClasses per block of
-// kSchedBlock windows), the one-wave slots and, given a window order, its
-// inverse.
-struct SchedScratch {
-    size_t tab, team, counts, sched, inv, bytes;
-};
-constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
-constexpr SchedScratch sched_scratch(int64_t W, bool ordered)
-{
-    auto up = round256;
-    SchedScratch l{};
-    l.tab = 0;
-    l.team = up(sizeof(SchedTables));
-    l.counts = l.team + up(sizeof(int32_t) * kHeavyMaxWindows);
-    l.sched = l.counts + up(sizeof(int32_t) * kSchedClasses * (size_t)ceil_div(W, kSchedBlock));
-    l.inv = l.sched + up(sizeof(int32_t) * kXcds * (size_t)sched_xcd_slots(W));
-    l.bytes = l.inv + (ordered ? up(sizeof(int32_t) * (size_t)W) : 0);
-    return l;
 }
 
 // f3s_attention_fwd; the scheduled launch takes its scratch from
@@ -1105,32 +1163,16 @@ static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const
         (!ordered || (int64_t)W * H >= kSchedOrderedMin)) {
         // the library's schedule (see sched_fill): heavy windows on teams of
         // 16 waves, the others on one wave each, by class, XCD by XCD
-        const SchedScratch lay = sched_scratch(W, ordered);
         StreamBuffer scratch(st);   // returned to the allocator in stream order, after the launches
         char* sp = static_cast<char*>(fixed_scratch);
         if (!sp) {
-            F3S_TRY(scratch.reserve(lay.bytes));
+            F3S_TRY(scratch.reserve(sched_scratch(W, ordered).bytes));
             sp = static_cast<char*>(scratch.ptr);
         }
-        SchedTables* tab = reinterpret_cast<SchedTables*>(sp + lay.tab);
-        int32_t* team = reinterpret_cast<int32_t*>(sp + lay.team);
-        int32_t* counts = reinterpret_cast<int32_t*>(sp + lay.counts);
-        int32_t* sched = reinterpret_cast<int32_t*>(sp + lay.sched);
-        int32_t* inv = ordered ? reinterpret_cast<int32_t*>(sp + lay.inv) : nullptr;
-        const int32_t nb = (int32_t)ceil_div(W, kSchedBlock);
+        int32_t *team = nullptr, *sched = nullptr;
+        F3S_TRY(launch_schedule(d_window_offsets, d_window_order, W, kHeavyMaxWindows, sp, st,
+                                &team, &sched));
         const int64_t L = sched_xcd_slots(W);
-        const int32_t fill_blocks = (int32_t)std::max<int64_t>(nb, ceil_div(kXcds * L, kSchedBlock));
-        if (ordered)
-            hipLaunchKernelGGL(sched_inverse, dim3((unsigned)nb), dim3(kSchedBlock), 0, st,
-                               d_window_order, W, inv);
-        hipLaunchKernelGGL(sched_count, dim3((unsigned)nb), dim3(kSchedBlock), 0, st,
-                           d_window_offsets, d_window_order, inv, W, nb, counts);
-        hipLaunchKernelGGL(sched_scan, dim3(1), dim3(1024), 0, st, counts, nb, tab);
-        hipLaunchKernelGGL(sched_fill, dim3((unsigned)fill_blocks), dim3(kSchedBlock), 0, st,
-                           d_window_offsets, d_window_order, inv, W, nb, counts, tab, (int32_t)L,
-                           team, sched);
-        const hipError_t le = hipGetLastError();
-        if (le != hipSuccess) return hip_fail(le, "window schedule", __FILE__, __LINE__);
         AttnParams ph = p;
         ph.window_order = team;
         ph.xcd_contiguous = 0;
@@ -1264,7 +1306,6 @@ f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_win
     }
     p->W = W;
     p->H = H;
-    p->natural_order = d_window_order == nullptr;
     // Automatic plans give tile-dense passes their own, finer item set (a
     // tile-dense chunk costs two whole tiles, ~15x a masked chunk per tile
     // on sparse graphs); graphs whose windows leave most SIMDs idle run teams
@@ -1449,7 +1490,7 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
     p.num_items = set.num_items;
     p.W = plan->W;
     p.n = n;
-    p.xcd_contiguous = plan->natural_order;
+    p.xcd_contiguous = plan->xcd_contiguous;
     p.partials = reinterpret_cast<float*>(plan->partials.ptr);
     p.splits = reinterpret_cast<const SplitInfo*>(set.splits.ptr);
     p.num_split = set.num_split;

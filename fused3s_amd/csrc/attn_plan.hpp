@@ -15,7 +15,8 @@ struct f3s_item_set {
 
 struct f3s_plan {
     int32_t W = 0, H = 1;
-    int32_t natural_order = 1;   // no window order given: keep neighbours on one XCD
+    int32_t xcd_contiguous = 1;  // items map to XCDs in contiguous ranges (scheduled
+                                 // items, or natural order: neighbours share an L2)
     int64_t T = 0;
     // Masked passes (compiled lists or tile expansion) run `masked`.  A
     // tile-dense chunk costs two whole tiles, about 15x a masked chunk per

@@ -205,7 +205,11 @@ f3s_status f3s_naive_attention_fwd(const float* Q, const float* K, const float* 
  * sort) or, when it is NULL, in natural order with consecutive windows kept
  * on one XCD (for community-ordered graphs).  Build once per graph; reuse for
  * every forward pass; one plan must not serve two overlapping calls (it owns
- * the partial-result buffers). */
+ * the partial-result buffers).  From 2^18 window-heads (W x H) on, a plan
+ * whose items run one wave each follows the library's schedule of
+ * f3s_attention_fwd instead of the order's sequence (the order then only
+ * names the windows), keeping a community-ordered graph's L2 reuse under the
+ * reference's descending order. */
 typedef struct f3s_plan f3s_plan;
 f3s_status f3s_plan_create(const int32_t* d_window_offsets, const int32_t* d_window_order,
                            int32_t W, int32_t H, int32_t seg_tiles, void* stream,

@@ -566,11 +566,11 @@ def test_unplanned_heavy_windows(gpu):
 
 
 def test_unplanned_schedule_names_windows(gpu):
-    # From 2^18 window-heads on, a window order only names the windows to
-    # compute, and the library's schedule runs them: invalid entries are
-    # skipped, a repeated window is computed once, windows the order does
-    # not name are left untouched, and every order gives the bits of a
-    # natural-order call.  4,096 windows x 64 heads; the hub windows 0, 2
+    # From 2^18 window-heads on (plans and the drop-in launch alike), a window
+    # order only names the windows to compute, and the library's schedule
+    # runs them: invalid entries are skipped, a repeated
+    # window is computed once, windows the order does not name are left
+    # untouched, and every order gives the bits of a natural-order call.  4,096 windows x 64 heads; the hub windows 0, 2
     # and 2,062 (rows of 3,000 random neighbours, over 1,024 tiles) take the
     # team launch wherever the order puts them.
     n, H = 65536, 64
@@ -627,6 +627,16 @@ def test_unplanned_schedule_names_windows(gpu):
         want = p.oracle(masked, rows=ranges)
         assert_close(np.concatenate([got[a:b] for a, b in ranges]),
                      np.concatenate([want[r] for r in ranges]), what)
+        # plans of a graph this size follow the same schedule (hub windows
+        # split into segments instead of teams): any order names the windows
+        pfull = p.run(masked, planned=True, compiled=masked)
+        pperm = p.run(masked, planned=True, order=dperm, compiled=masked)
+        ppart = p.run(masked, planned=True, order=dorder, compiled=masked)
+        assert np.array_equal(pperm.view(np.uint32), pfull.view(np.uint32)), what
+        assert np.all(np.isnan(ppart[~rows])), what
+        assert np.array_equal(ppart[rows].view(np.uint32), pfull[rows].view(np.uint32)), what
+        assert_close(np.concatenate([pfull[a:b] for a, b in ranges]),
+                     np.concatenate([want[r] for r in ranges]), what + " planned")
 
 
 def test_unplanned_natural_order_heavy_cap(gpu):
