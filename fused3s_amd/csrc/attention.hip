@@ -508,7 +508,7 @@ constexpr int kSchedClasses = 64;   // 32 octaves of the tile count, x {heavy, n
 // call, 5 % of config 4's pass (62,500 window-heads, which keeps the order's
 // sequence) and under 1.5 % from here on.
 constexpr int64_t kSchedOrderedMin = (int64_t)1 << 18;
-constexpr int kSchedBlock = 256;    // windows per block of sched_count / sched_fill
+constexpr int kSchedBlock = 1024;   // windows per block of sched_count / sched_fill
 
 struct SchedTables {
     int32_t size[kSchedClasses];               // windows per class outside the team list
@@ -583,7 +583,7 @@ sched_count(const int32_t* __restrict__ window_offsets, const int32_t* __restric
 // kernel earlier, so every load goes below L2: each class's row is cut into
 // 16 contiguous segments, one per lane of a 16-lane row, and a lane loads its
 // segment in one batch (kept in registers for the rewrite when it holds at
-// most kSegRegs values: graphs of up to 131,072 windows), scans the
+// most kSegRegs values: graphs of up to 524,288 windows), scans the
 // 16 sums with its row and writes its segment's offsets.  The tables come
 // from wave-wide scans over the classes.
 constexpr int kScanSegs = 16;

@@ -163,7 +163,7 @@ f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_
  * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
  * semantics, kernels and results (bit for bit) as f3s_attention_fwd; the
  * schedule's scratch (tables, team list, class counts, one-wave slots and an
- * order's inverse: 18 MiB) is a fixed device array of the library, one per
+ * order's inverse: 16.5 MiB) is a fixed device array of the library, one per
  * GPU, held until the process ends.  Limit: W <= 2,097,152 row windows
  * (n <= 33,554,432 nodes); larger W returns F3S_EUNSUPPORTED.  Every call on
  * one GPU shares that GPU's array and overwrites it, so calls that overlap in

@@ -644,10 +644,10 @@ def test_unplanned_natural_order_heavy_cap(gpu):
     # 16,800) hold exactly 600 tiles, a class of their own ([512, 1024)
     # tiles) that the one-wave launch starts first, cut into eight XCD
     # shares; the threshold for teams, max(1024, 8 x mean) = 1,208 tiles,
-    # takes none of them.  The class spans all 66 of the schedule's
-    # 256-window blocks, 64 windows in each.  The sorted order runs in its
-    # own sequence (no team either).  Results meet the oracle, both orders
-    # give the same bits, and repeated runs too.
+    # takes none of them.  The class spans all 17 of the schedule's
+    # 1,024-window blocks (256 windows in each but the last).  The sorted
+    # order runs in its own sequence (no team either).  Results meet the
+    # oracle, both orders give the same bits, and repeated runs too.
     W = 16_800
     n = 16 * W
     heavy_w = np.arange(4200) * 4
