@@ -3,7 +3,10 @@ density with optional hub rows and isolated nodes, converted bit-exactly,
 then random head counts and scales through every launch shape -- unplanned in natural, sorted and random window
 order, automatic plans (teams on small graphs), plans with small forced
 segments, compiled lists -- in both semantics, against the CPU oracle at the
-north-star bar (max abs 2e-3, normwise max rel 1e-2).
+north-star bar (max abs 2e-3, normwise max rel 1e-2).  A second sweep draws
+sparser graphs of 513 to 2,000 windows, where the unplanned launch in
+natural order runs on the library's schedule (classes of tile count, XCD
+shares, a team launch for the heavy windows).
 """
 from __future__ import annotations
 
@@ -18,9 +21,9 @@ pytestmark = pytest.mark.gpu
 ABS_TOL, REL_TOL = 2e-3, 1e-2
 
 
-def random_graph(r: np.random.Generator):
-    n = int(r.integers(1, 6000))
-    deg = float(r.uniform(0, 24))
+def random_graph(r: np.random.Generator, n_range=(1, 6000), deg_max: float = 24.0):
+    n = int(r.integers(*n_range))
+    deg = float(r.uniform(0, deg_max))
     m = int(n * deg / 2)
     u = r.integers(0, n, m)
     v = r.integers(0, n, m)
@@ -44,8 +47,19 @@ def random_graph(r: np.random.Generator):
 def test_random_parity(gpu, seed):
     r = rng(1000 + seed)
     rp, ci = random_graph(r)
+    check_parity(gpu, seed, r, rp, ci, int(r.choice([1, 1, 2, 3, 4])))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_parity_scheduled(gpu, seed):
+    r = rng(5000 + seed)
+    rp, ci = random_graph(r, (8208, 32000), 6.0)
+    assert (len(rp) - 1 + 15) // 16 > 512
+    check_parity(gpu, 5000 + seed, r, rp, ci, int(r.choice([1, 2])))
+
+
+def check_parity(gpu, seed, r, rp, ci, H):
     n = len(rp) - 1
-    H = int(r.choice([1, 1, 2, 3, 4]))
     scale = float(r.choice([1.0, 0.125, 0.5]))
     Q, K, V = (r.standard_normal((n, H, 64)).astype(np.float16) for _ in range(3))
     bsf = gpu.convert_device(gpu.DeviceCSR(rp, ci))
