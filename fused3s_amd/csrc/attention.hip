@@ -1159,11 +1159,13 @@ static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const
     p.xcd_contiguous = d_window_order == nullptr;
     hipStream_t st = as_stream(stream);
     const bool ordered = d_window_order != nullptr;
+    // The schedule's scratch: returned to the allocator in stream order when
+    // this function returns, i.e. after the last launch that reads it.
+    StreamBuffer scratch(st);
     if (p.team == 1 && !wide_features(n, H) && W > kHeavyMaxWindows &&
         (!ordered || (int64_t)W * H >= kSchedOrderedMin)) {
         // the library's schedule (see sched_fill): heavy windows on teams of
         // 16 waves, the others on one wave each, by class, XCD by XCD
-        StreamBuffer scratch(st);   // returned to the allocator in stream order, after the launches
         char* sp = static_cast<char*>(fixed_scratch);
         if (!sp) {
             F3S_TRY(scratch.reserve(sched_scratch(W, ordered).bytes));

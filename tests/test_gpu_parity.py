@@ -532,6 +532,51 @@ def test_concurrent_converter_and_natural_order_launch(gpu):
         assert np.array_equal(out.view(np.uint32), wants[k].view(np.uint32))
 
 
+def test_schedule_scratch_outlives_its_launches(gpu):
+    # Two natural-order drop-in calls on two streams, back to back with no
+    # synchronisation, on two graphs of the same size (so the second call's
+    # schedule scratch is the block the first returned to the allocator) but
+    # different edges (so their schedules differ): the first call's scratch
+    # must go back only after its last launch, or the second call's schedule
+    # overwrites the slots the first call's one-wave launch still reads.  The
+    # first call is tile-dense (a long launch whose later waves start late),
+    # the second masked (short).  Every result equals a call run alone.
+    # (A build that returned the scratch before the last launch was enqueued
+    # also passed here: the race needs the second stream's schedule kernels
+    # to run while the first launch still starts waves, which this run never
+    # showed; the ordering itself is shown by reading attention_fwd_impl.)
+    n = 200_000
+    probs = []
+    for k in range(2):
+        r = rng(90 + k)
+        m = 8 * n
+        u, v = r.integers(0, n, m), r.integers(0, n, m)
+        if k == 1:
+            v = (u + r.integers(0, 4096, m)) % n          # local edges: other tile counts
+        key = np.unique(np.concatenate([u, v, np.arange(n)]).astype(np.int64) * n +
+                        np.concatenate([v, u, np.arange(n)]))
+        rp = np.zeros(n + 1, np.int64)
+        np.add.at(rp, key // n + 1, 1)
+        probs.append(Problem(gpu, np.cumsum(rp).astype(np.int32), (key % n).astype(np.int32),
+                             H=1, seed=92 + k))
+    sems = (False, True)
+    wants = [p.run(m) for p, m in zip(probs, sems)]
+    streams = [gpu.Stream(), gpu.Stream()]
+    outs = [gpu.DeviceArray((n, 1, 64), np.float32) for _ in range(2)]
+    for rep in range(4):
+        for k in range(2):
+            outs[k].fill_bytes(0xFF)
+        gpu.synchronize()
+        for k in range(2):
+            p = probs[k]
+            gpu.attention_fwd(p.dQ, p.dK, p.dV, outs[k], p.bsf, None, masked=sems[k], H=1,
+                              stream=streams[k])
+        gpu.synchronize()
+        for k in range(2):
+            got = outs[k].numpy()
+            assert np.array_equal(got.view(np.uint32), wants[k].view(np.uint32)), (rep, k)
+
+
 def test_unplanned_heavy_windows(gpu):
     # Without a plan, windows of more than max(1024, 8 x mean) tiles run as
     # 16-wave teams in a launch of their own -- in natural order (the
