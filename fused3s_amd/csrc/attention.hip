@@ -490,10 +490,16 @@ hipError_t warm_attention(hipStream_t s)
 //   * every other window on one wave, by class of tile count (the octave;
 //     heavy windows past the team list form the first classes), heaviest
 //     class first, each class in index order and cut into eight contiguous
-//     shares, one per XCD.  XCD x runs its share of every class in class
-//     order: the longest windows start first and only the smallest finish
-//     last, and each XCD walks a contiguous range of windows within a class,
-//     which keeps a community-ordered graph's neighbours in its L2.
+//     shares; slot i * 8 + x holds share x's i-th window, and the launch
+//     deals its workgroups to the XCDs round-robin.  The longest windows
+//     start first and only the smallest finish last, and each share -- a
+//     contiguous range of windows -- runs on one XCD when a workgroup is one
+//     window (4 heads) or on a few, which keeps a community-ordered graph's
+//     neighbours in their L2s.  (Each XCD's workgroups taking its share as a
+//     contiguous range of slots measured the same on config 5 but 10 %
+//     slower on a plan of config 4 and 3 % with 8 heads; one sequence of the
+//     classes dealt round-robin, with no shares, ran config 5 13 % slower
+//     tile-dense, its communities fetched into every L2.)
 // Four small kernels build it, and no memory needs clearing first (so the
 // launch may be captured into a graph): sched_inverse (an order's inverse,
 // scattered: window w is named iff inv[w] is a position that holds w, which
@@ -514,14 +520,13 @@ struct SchedTables {
     int32_t size[kSchedClasses];               // windows per class outside the team list
     int32_t taken[kSchedClasses];              // windows per class in the team list
     int32_t team_base[kSchedClasses];          // team-list position of a class's first window
-    int32_t xcd_base[kXcds][kSchedClasses];    // XCD x's slots before its share of a class
-    int32_t xcd_items[kXcds];                  // XCD x's slots in use
+    int32_t xcd_base[kXcds][kSchedClasses];    // share x's windows before its part of a class
+    int32_t xcd_items[kXcds];                  // share x's windows
     int32_t team_items;                        // team-list entries in use
 };
 
-// Slots per XCD in the one-wave launch: past any XCD's share of W windows
-// (each class share rounds up by at most one), a multiple of 4 so that every
-// XCD's slots fill whole 4-wave workgroups.
+// Slots per XCD share in the one-wave launch: past any share of W windows
+// (each class share rounds up by at most one), a multiple of 4.
 constexpr int64_t sched_xcd_slots(int64_t W)
 {
     return (ceil_div(W, kXcds) + kSchedClasses + 3) / 4 * 4;
@@ -665,9 +670,9 @@ sched_scan(int32_t* __restrict__ counts, int32_t nb, int32_t team_cap, SchedTabl
     }
 }
 
-// Slots: the team list (kHeavyMaxWindows entries) and, per XCD, L one-wave
-// slots; a class's windows keep their index order (stable ranks within a
-// block from wave ballots).
+// Slots: the team list (kHeavyMaxWindows entries) and 8 L one-wave slots, slot
+// i * 8 + x the i-th window of share x; a class's windows keep their index
+// order (stable ranks within a block from wave ballots).
 __global__ void __launch_bounds__(kSchedBlock)
 sched_fill(const int32_t* __restrict__ window_offsets, const int32_t* __restrict__ order,
            const int32_t* __restrict__ inv, int32_t W, int32_t nb,
@@ -677,7 +682,7 @@ sched_fill(const int32_t* __restrict__ window_offsets, const int32_t* __restrict
     __shared__ int32_t wc[kSchedBlock / kWave][kSchedClasses];
     const int t = threadIdx.x, lane = t & (kWave - 1), wid = t / kWave;
     const int64_t g = (int64_t)blockIdx.x * kSchedBlock + t;
-    if (g < (int64_t)kXcds * L && g % L >= tab->xcd_items[g / L]) sched[g] = -1;
+    if (g < (int64_t)kXcds * L && g / kXcds >= tab->xcd_items[g % kXcds]) sched[g] = -1;
     if (g < kHeavyMaxWindows && g >= tab->team_items) team[g] = -1;
     if ((int32_t)blockIdx.x >= nb) return;   // uniform
     const int32_t heavy = heavy_tiles(window_offsets[W], W, kHeavyMinTiles, kHeavyMeanFactor);
@@ -706,7 +711,7 @@ sched_fill(const int32_t* __restrict__ window_offsets, const int32_t* __restrict
     }
     const int64_t sz = tab->size[q], r2 = r - take;
     const int64_t x = (kXcds * r2 + kXcds - 1) / sz;   // its share: [sz x / 8, sz (x + 1) / 8)
-    sched[x * L + tab->xcd_base[x][q] + (r2 - sz * x / kXcds)] = w;
+    sched[(tab->xcd_base[x][q] + (r2 - sz * x / kXcds)) * kXcds + x] = w;
 }
 
 // Scratch of the scheduled launch for W windows, in 256-byte sections: the
@@ -733,7 +738,8 @@ constexpr SchedScratch sched_scratch(int64_t W, bool ordered)
 // Builds the schedule of W windows (those `order` names, or all) into scratch
 // `sp` laid out by sched_scratch(W, order != NULL): a team list of at most
 // team_cap heavy windows (kHeavyMaxWindows entries, -1 past its end) and
-// kXcds * L one-wave slots (-1 where empty), L = sched_xcd_slots(W).
+// kXcds * L one-wave slots (-1 where empty), L = sched_xcd_slots(W), to be
+// dealt to the XCDs round-robin.
 static f3s_status launch_schedule(const int32_t* d_window_offsets, const int32_t* d_window_order,
                                   int32_t W, int32_t team_cap, char* sp, hipStream_t st,
                                   int32_t** team_out, int32_t** sched_out)
@@ -957,11 +963,12 @@ namespace f3s {
 // buffer is shared by the sets (a plan serves one pass at a time).  From
 // kSchedOrderedMin window-heads on, with one wave per item (no teams), the
 // items follow the drop-in launch's schedule (classes of tile count,
-// heaviest first, eight contiguous XCD shares; no team list: heavy windows
-// are split into segments) and the pass maps them XCD-contiguously, whatever
-// the window order; otherwise they follow the order's sequence.  (On config
-// 4, 62,500 window-heads, the schedule's layout measured 9 % slower than the
-// descending order's sequence: 597 against 548 us per planned pass.)
+// heaviest first, eight interleaved XCD shares; no team list: heavy windows
+// are split into segments), dealt round-robin, whatever the window order;
+// otherwise they follow the order's sequence.  (On config 4, 62,500
+// window-heads, the schedule measured 1-2 % slower than the descending
+// order's sequence: 562 against 558 us masked, 8.96 against 8.76 ms
+// tile-dense.)
 static f3s_status build_plan_sets(f3s_plan* p, const int32_t* d_window_offsets,
                                   const int32_t* d_window_order, int32_t seg_tiles,
                                   hipStream_t st)
@@ -986,7 +993,7 @@ static f3s_status build_plan_sets(f3s_plan* p, const int32_t* d_window_offsets,
         seq = sched;
         P = (int32_t)(kXcds * sched_xcd_slots(W));
     }
-    p->xcd_contiguous = scheduled || d_window_order == nullptr;
+    p->xcd_contiguous = !scheduled && d_window_order == nullptr;
     const size_t cnt_bytes = sizeof(int32_t) * (size_t)arrays * (size_t)P;
     const size_t base_bytes = sizeof(int64_t) * (size_t)arrays * ((size_t)P + 1);
     const size_t tmp_bytes = sizeof(int64_t) * (size_t)scan_tmp_elems(P);
@@ -1182,7 +1189,7 @@ static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const
         ph.num_items = (int64_t)kHeavyMaxWindows * kTeamLarge;
         F3S_TRY(launch(ph, H, scale, st));
         p.window_order = sched;
-        p.xcd_contiguous = 1;
+        p.xcd_contiguous = 0;
         p.num_items = kXcds * L;
     } else if (p.team == 1 && ordered && !wide_features(n, H)) {
         // The order's sequence: teams of 16 waves for the heavy windows among

@@ -144,10 +144,11 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * identically for every order: the heavy windows, heaviest first, the first
  * 512 of them as teams of 16 waves in a launch of their own; every other
  * window on one wave, by octave of its tile count, heaviest first, each
- * octave in index order and cut into eight contiguous shares, one per XCD
- * (longest windows first for the tail, contiguous windows per XCD for the
- * L2; on a community-ordered graph the reference's descending order would
- * scatter each community over the whole run).  Four small kernels (~30 us)
+ * octave in index order and cut into eight contiguous shares interleaved
+ * slot by slot across the XCDs (longest windows first for the tail, each
+ * share's contiguous windows on one or a few XCDs for the L2; on a
+ * community-ordered graph the reference's descending order would scatter
+ * each community over the whole run).  Four small kernels (~30 us)
  * build the schedule in scratch of about 9 bytes per window taken from the
  * library's pool and returned to it in stream order on `stream` (the call
  * does not wait).  Tensors past ~4 GiB take the sequence of the order, as
