@@ -310,6 +310,24 @@ def test_attention_random_heads(gpu, H, n, deg, seed):
                                     f"compiled={compiled}")
 
 
+@pytest.mark.parametrize("H", [33, 64])
+@pytest.mark.parametrize("n,deg,seed", [(37, 5, 5), (500, 12, 6)])
+def test_attention_many_heads(gpu, H, n, deg, seed):
+    # up to the 64 heads the API accepts (and an odd count past 32), every
+    # launch shape, both semantics
+    rp, ci = random_csr(n, deg, seed, self_loops=True)
+    p = Problem(gpu, rp, ci, H=H, normal=True, seed=seed)
+    order = gpu.window_order_device(p.bsf)
+    for masked in (True, False):
+        want = p.oracle(masked, scale=0.125)
+        for planned, compiled in ((False, False), (True, False), (True, True)):
+            got = p.run(masked, planned=planned, seg=4, scale=0.125, compiled=compiled and masked)
+            assert_close(got, want, f"n={n} H={H} masked={masked} planned={planned} "
+                                    f"compiled={compiled}")
+        got = p.run(masked, order=order, scale=0.125)
+        assert_close(got, want, f"n={n} H={H} masked={masked} ordered")
+
+
 @pytest.mark.parametrize("case,H,team_m,team_d", [("random", 1, 4, 16), ("random", 4, 4, 4),
                                                  ("random", 8, 1, 4), ("random", 16, 1, 1),
                                                  ("star", 1, 4, 16), ("star", 3, 4, 4)])
