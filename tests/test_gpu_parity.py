@@ -963,3 +963,70 @@ def test_config5_full_size(gpu):
 
     check_sampled("cfg5 tile-dense plan", run(lambda: plan.forward(dQ, dK, dV, dO, masked=False)),
                   ranges, want_rows)
+
+
+@pytest.mark.slow
+def test_schedule_on_a_graph_of_550_count_blocks(gpu):
+    """9,000,000 nodes (562,500 windows; also past the converter's
+    one-bitmap limit): the schedule's class counts span 550 blocks, more
+    than sched_scan keeps in registers, so it takes its two-pass segment
+    loop.  Masked attention on every row for the drop-in launch in natural
+    order (three hub windows of ~20,000 tiles on 16-wave teams) and a
+    compiled plan (on the same schedule); the drop-in launch in descending
+    order (562,500 window-heads: the schedule too) and the allocation-free
+    entry point give the natural-order bits, a plan given the order those of
+    a plan without it; tile-dense on sampled rows."""
+    from fused3s_amd import _lib
+    n = 9_000_000
+    r = rng(97)
+    rows = [np.arange(n), np.repeat(np.arange(n), 2)]
+    cols = [np.arange(n), r.integers(0, n, 2 * n)]
+    hubs = (5, 4_500_017, 8_999_999)
+    for hub in hubs:
+        rows.append(np.full(20000, hub))
+        cols.append(r.integers(0, n, 20000))
+    key = np.unique(np.concatenate(rows).astype(np.int64) * n + np.concatenate(cols))
+    del rows, cols
+    rp = np.zeros(n + 1, np.int64)
+    rp[1:] = np.cumsum(np.bincount(key // n, minlength=n))
+    rp, ci = rp.astype(np.int32), (key % n).astype(np.int32)
+    del key
+    p = Problem(gpu, rp, ci, H=1, seed=98, f32=True)
+    bsf = p.bsf
+    W = bsf.W
+    tiles = np.diff(bsf.window_offsets.numpy())
+    thr = max(1024, 8 * (-(-int(tiles.sum()) // W)))
+    assert -(-W // 1024) == 550 and list(np.nonzero(tiles > thr)[0]) == [h // 16 for h in hubs]
+    log(f"550 count blocks: n={n} nnz={len(ci)} W={W} T={int(tiles.sum())}")
+    order = gpu.window_order_device(bsf)
+    th = oracle_threads()
+    t0 = time.time()
+    want = orc.masked_attention(n, 64, 1, p.Qf, p.Kf, p.Vf, rp, ci, 1.0, threads=th)
+    log(f"  masked oracle, whole graph: {time.time()-t0:.2f}s on {th} threads")
+    nat = p.run(True)
+    check_whole_graph("drop-in, natural order", nat, want)
+    got = p.run(True, order=order)
+    assert np.array_equal(got.view(np.uint32), nat.view(np.uint32)), "descending order"
+    p.dO.fill_bytes(0xFF)
+    assert _lib.hip().f3s_attention_fwd_noalloc(
+        p.dQ.ptr, p.dK.ptr, p.dV.ptr, p.dO.ptr, bsf.window_offsets.ptr, bsf.block_col.ptr,
+        bsf.tile_mask.ptr, None, W, n, 64, 1, 1.0, None) == 0
+    gpu.synchronize()
+    assert np.array_equal(p.dO.numpy().view(np.uint32), nat.view(np.uint32)), "noalloc"
+    del got, nat
+    pl = p.run(True, planned=True, compiled=True)
+    check_whole_graph("compiled plan", pl, want)
+    got = p.run(True, planned=True, compiled=True, order=order)
+    assert np.array_equal(got.view(np.uint32), pl.view(np.uint32)), "plan, descending order"
+    del got, pl, want
+    hb = p.host_bsf()
+    ranges = sample_rows(hb, n, stride_rows=60000)
+
+    def want_rows(a, b):
+        return orc.tile_dense_attention(n, 64, 1, p.Qf, p.Kf, p.Vf, hb.window_offsets,
+                                        hb.block_col_indices, 1.0, a, b, threads=th)[a:b]
+
+    nat = p.run(False)
+    check_sampled("tile-dense drop-in, natural order", nat, ranges, want_rows)
+    got = p.run(False, order=order)
+    assert np.array_equal(got.view(np.uint32), nat.view(np.uint32)), "tile-dense, descending"
