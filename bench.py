@@ -194,6 +194,18 @@ def gather_ceiling(f3s, dK, dV, rows: int, H: int, count: int, stream, reps: int
             "table_bytes_each": rows * stride}
 
 
+def host_cpu_model() -> str:
+    """The host CPU's model name (first processor of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(rp, ci, Q, K, V, n: int, d: int) -> dict | None:
     """The reference's cpu_sparse_attention_csr (single thread) over the
     whole graph, on this host."""
@@ -214,7 +226,9 @@ def cpu_baseline(rp, ci, Q, K, V, n: int, d: int) -> dict | None:
     edges = int(rp[n])
     return {"value": edges / dt, "unit": "edges/s", "cores": 1, "kind": kind,
             "sample": f"all {n} rows / {edges} edges of the workload, one call, "
-                      f"{dt:.2f} s on {os.cpu_count()} visible host cores (1 used)"}
+                      f"{dt:.2f} s on {os.cpu_count()} visible host cores (1 used)",
+            "threads_used": 1, "cores_available": len(os.sched_getaffinity(0)),
+            "cpu_model": host_cpu_model()}
 
 
 def cpu_baseline_all_cores(rp, ci, Q, K, V, n: int, H: int, d: int) -> dict | None:
@@ -241,7 +255,9 @@ def cpu_baseline_all_cores(rp, ci, Q, K, V, n: int, H: int, d: int) -> dict | No
     edges = int(rp[n])
     return {"value": edges / dt, "unit": "edges/s", "cores": threads, "kind": "port",
             "sample": f"all {n} rows / {edges} edges x {H} head(s), one call, {dt:.2f} s on "
-                      f"{threads} threads (OpenMP) of {len(os.sched_getaffinity(0))} available cores"}
+                      f"{threads} threads (OpenMP) of {len(os.sched_getaffinity(0))} available cores",
+            "threads_used": threads, "cores_available": len(os.sched_getaffinity(0)),
+            "cpu_model": host_cpu_model()}
 
 
 def main() -> int:

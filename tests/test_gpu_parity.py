@@ -38,10 +38,25 @@ def errors(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
     return mabs, (mabs / scale if scale > 0 else mabs)
 
 
+def elem_rel(got: np.ndarray, want: np.ndarray, floor: float = 0.1) -> float:
+    """Largest elementwise relative error over the elements with |c| >= floor
+    (reported for information; the bars are max_abs and the normwise max_rel)."""
+    g, w = got.reshape(-1), want.reshape(-1)
+    out = 0.0
+    for i in range(0, g.size, 1 << 24):
+        wi = w[i:i + (1 << 24)].astype(np.float64)
+        big = np.abs(wi) >= floor
+        if big.any():
+            gi = g[i:i + (1 << 24)].astype(np.float64)
+            out = max(out, float((np.abs(gi[big] - wi[big]) / np.abs(wi[big])).max()))
+    return out
+
+
 def assert_close(got, want, what=""):
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     mabs, mrel = errors(got, want)
-    log(f"  {what}: max_abs={mabs:.3e} max_rel={mrel:.3e}")
+    log(f"  {what}: max_abs={mabs:.3e} max_rel={mrel:.3e} "
+        f"(elementwise rel, |c| >= 0.1: {elem_rel(got, want):.3e})")
     assert mabs <= ABS_TOL and mrel <= REL_TOL, f"{what}: max_abs={mabs:.3e} max_rel={mrel:.3e}"
 
 
@@ -840,7 +855,8 @@ def errors_chunked(got: np.ndarray, want: np.ndarray, chunk: int = 1 << 24) -> t
 def check_whole_graph(what: str, got: np.ndarray, want: np.ndarray) -> None:
     assert np.all(np.isfinite(got)), f"{what}: unwritten or non-finite rows"
     mabs, mrel = errors_chunked(got, want)
-    log(f"  {what}: every row, max_abs={mabs:.3e} max_rel={mrel:.3e}")
+    log(f"  {what}: every row, max_abs={mabs:.3e} max_rel={mrel:.3e} "
+        f"(elementwise rel, |c| >= 0.1: {elem_rel(got, want):.3e})")
     assert mabs <= ABS_TOL and mrel <= REL_TOL, f"{what}: {mabs} {mrel}"
 
 
