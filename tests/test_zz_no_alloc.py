@@ -4,9 +4,11 @@ f3s_attention_fwd on the same inputs: bit-identical outputs, both within the
 north-star tolerance of the oracle, over two calls in a row on graphs whose
 heavy windows take the schedule's team launch -- the second graph smaller,
 so stale scratch from the first call would show -- in both semantics, in
-natural order and in an order's sequence; and the size limit.  (The
-scheduled launch with a window order, whose inverse lives in the same
-scratch, is compared in test_gpu_parity.py's
+natural order and in an order's sequence; the size limit; and replays from
+a captured HIP graph, in natural order and -- with 2^18 window-heads, where
+the schedule runs an order's windows and keeps the order's inverse in the
+same scratch -- in the reference's descending order.  (That scheduled
+launch with a partial order is compared in test_gpu_parity.py's
 test_unplanned_schedule_names_windows.)"""
 from __future__ import annotations
 
@@ -87,37 +89,59 @@ def test_noalloc_rejects_graphs_past_its_scratch(gpu):
     assert st == 5 and b"2097152" in lib.f3s_last_error()
 
 
+def replay_matches_eager(gpu, torch, lib, p, masked: bool, order=None) -> None:
+    """Captures the allocation-free launch into a graph and replays it three
+    times, with eager library work and synchronisations between the replays:
+    every replay must reproduce the eager result of the allocating entry
+    point bit for bit."""
+    bsf = p.bsf
+    other = gpu.DeviceArray(p.dO.shape, np.float32)
+    args = (p.dQ.ptr, p.dK.ptr, p.dV.ptr, p.dO.ptr, bsf.window_offsets.ptr, bsf.block_col.ptr,
+            bsf.tile_mask.ptr if masked else None, order.ptr if order is not None else None,
+            bsf.W, bsf.n, 64, p.H, 0.125)
+    want = call(lib.f3s_attention_fwd, p, masked, order)   # eager, allocating entry point
+    st = lib.f3s_attention_fwd_noalloc(*args, None)         # eager warm-up of the variant
+    assert st == 0
+    gpu.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = lib.f3s_attention_fwd_noalloc(*args, torch.cuda.current_stream().cuda_stream)
+    assert st == 0, lib.f3s_last_error()
+    what = (masked, order is not None)
+    for rep in range(3):
+        p.dO.fill_bytes(0xFF)
+        # eager work between replays: the same pass into another buffer
+        assert lib.f3s_attention_fwd(*args[:3], other.ptr, *args[4:], None) == 0
+        gpu.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = p.dO.numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (what, rep)
+        assert np.array_equal(other.numpy().view(np.uint32), want.view(np.uint32)), (what, rep)
+    del g
+
+
 def test_noalloc_replays_from_a_hip_graph(gpu):
     # The allocation-free launch captured into a graph (no allocation, no
-    # host synchronisation and no memset in it) and replayed three times,
-    # with eager library work and synchronisations between the replays:
-    # every replay must reproduce the eager result bit for bit.
+    # host synchronisation and no memset in it): natural order, both
+    # semantics, on a graph whose heavy windows take the team launch.
     torch = pytest.importorskip("torch")
     from fused3s_amd import _lib
     lib = _lib.hip()
     rp, ci = hub_graph(40000, 83, {11: 30000, 20000: 1000, 30001: 25000})
     p = Problem(gpu, rp, ci, H=2, normal=True, seed=83)
-    bsf = p.bsf
-    other = gpu.DeviceArray(p.dO.shape, np.float32)
     for masked in (True, False):
-        args = (p.dQ.ptr, p.dK.ptr, p.dV.ptr, p.dO.ptr, bsf.window_offsets.ptr, bsf.block_col.ptr,
-                bsf.tile_mask.ptr if masked else None, None, bsf.W, bsf.n, 64, p.H, 0.125)
-        want = call(lib.f3s_attention_fwd, p, masked)       # eager, allocating entry point
-        st = lib.f3s_attention_fwd_noalloc(*args, None)     # eager warm-up of the variant
-        assert st == 0
-        gpu.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            st = lib.f3s_attention_fwd_noalloc(*args, torch.cuda.current_stream().cuda_stream)
-        assert st == 0, lib.f3s_last_error()
-        for rep in range(3):
-            p.dO.fill_bytes(0xFF)
-            # eager work between replays: the same pass into another buffer
-            assert lib.f3s_attention_fwd(*args[:3], other.ptr, *args[4:], None) == 0
-            gpu.synchronize()
-            g.replay()
-            torch.cuda.synchronize()
-            got = p.dO.numpy()
-            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (masked, rep)
-            assert np.array_equal(other.numpy().view(np.uint32), want.view(np.uint32))
-        del g
+        replay_matches_eager(gpu, torch, lib, p, masked)
+
+
+def test_noalloc_replays_an_ordered_schedule_from_a_hip_graph(gpu):
+    # 4,096 windows x 64 heads = 2^18 window-heads: a window order only names
+    # the windows and the schedule runs them, its inverse (sched_inverse)
+    # captured with the rest; the reference's descending order, masked.
+    torch = pytest.importorskip("torch")
+    from fused3s_amd import _lib
+    lib = _lib.hip()
+    rp, ci = hub_graph(65536, 84, {3: 3000, 40000: 3000})
+    p = Problem(gpu, rp, ci, H=64, seed=84, f32=True)
+    assert p.bsf.W * p.H >= 1 << 18
+    replay_matches_eager(gpu, torch, lib, p, True, gpu.window_order_device(p.bsf))
