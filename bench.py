@@ -174,14 +174,26 @@ def time_passes(f3s, one_pass, stream, reps: int) -> np.ndarray:
 
 
 def gather_ceiling(f3s, dK, dV, rows: int, H: int, count: int, stream, reps: int = 10,
-                   seed: int = 11) -> dict:
+                   seed: int = 11, pattern: str = "uniform") -> dict:
     """The device's random-gather ceiling for the pass's load shape
-    (f3s_probe_gather): `count` columns (rounded down to 32) of uniformly
-    random rows < `rows`, the K and V row of head 0 of each, on the
-    workload's own tensors; mean of `reps` launches timed with events on
-    `stream`."""
+    (f3s_probe_gather): `count` columns (rounded down to 32) of rows < `rows`,
+    the K and V row of head 0 of each, on the workload's own tensors; mean of
+    `reps` launches timed with events on `stream`.  Rows: uniformly random
+    ("uniform", a masked pass's columns), runs of 16 consecutive rows from
+    random multiples of 16 ("tile16", a tile-dense pass's tiles) or in order
+    ("stream")."""
     count = max(32, count // 32 * 32)
-    idx = np.random.default_rng(seed).integers(0, rows, count, dtype=np.int64).astype(np.int32)
+    g = np.random.default_rng(seed)
+    if pattern == "uniform":
+        idx = g.integers(0, rows, count, dtype=np.int64)
+    elif pattern == "tile16":
+        runs = g.integers(0, rows // 16, (count + 15) // 16, dtype=np.int64)
+        idx = (runs[:, None] * 16 + np.arange(16)[None, :]).reshape(-1)[:count]
+    elif pattern == "stream":
+        idx = np.arange(count, dtype=np.int64) % rows
+    else:
+        raise ValueError(pattern)
+    idx = idx.astype(np.int32)
     didx = f3s.DeviceArray.from_numpy(idx, stream)
     cpw = 8
     out = f3s.DeviceArray(((count // 32 + cpw - 1) // cpw,), np.uint32)
@@ -191,7 +203,7 @@ def gather_ceiling(f3s, dK, dV, rows: int, H: int, count: int, stream, reps: int
     mean = float(t.mean())
     return {"rows_per_s": 2 * count / (mean * 1e-3), "GBps": 2 * count * 128 / (mean * 1e-3) / 1e9,
             "probe_us": mean * 1e3, "columns": count, "table_rows": rows,
-            "table_bytes_each": rows * stride}
+            "table_bytes_each": rows * stride, "pattern": pattern}
 
 
 def host_cpu_model() -> str:
@@ -328,14 +340,17 @@ def main() -> int:
     if args.gather_probe:
         # uniformly random 128-byte K and V rows, the config-4 pass's column
         # count, tables from L2-resident (1 MB each) to past the Infinity
-        # Cache (512 MB each)
+        # Cache (512 MB each); on the 1,000,000-row tables also 16-row runs
+        # (a tile-dense pass's tiles) and rows in order
         f3s.init()
         stream = f3s.Stream()
         for rows in (8192, 1_000_000, 4_000_000):
             tk = f3s.DeviceArray((rows, 64), np.uint16, zero=True)
             tv = f3s.DeviceArray((rows, 64), np.uint16, zero=True)
-            r = gather_ceiling(f3s, tk, tv, rows, 1, 16_907_486, stream, reps=max(3, args.steps))
-            print(json.dumps({"gather_probe": r}), flush=True)
+            for pattern in ("uniform", "tile16", "stream") if rows == 1_000_000 else ("uniform",):
+                r = gather_ceiling(f3s, tk, tv, rows, 1, 16_907_486, stream,
+                                   reps=max(3, args.steps), pattern=pattern)
+                print(json.dumps({"gather_probe": r}), flush=True)
             del tk, tv
         return 0
     f3s.init()
@@ -527,11 +542,22 @@ def main() -> int:
     # count, beside the rate at which the pass gathers rows
     rows_pass = 2 * H * (occ_sum if masked else bsf.T * 16)
     gc = gather_ceiling(f3s, dK, dV, n, H, occ_sum, stream)
+    gc["tile16_rows_per_s"] = gather_ceiling(f3s, dK, dV, n, H, occ_sum, stream,
+                                             pattern="tile16")["rows_per_s"]
+    gc["stream_rows_per_s"] = gather_ceiling(f3s, dK, dV, n, H, occ_sum, stream,
+                                             pattern="stream")["rows_per_s"]
+
+    def ceiling(sem_masked: bool) -> float:
+        return gc["rows_per_s"] if sem_masked else gc["tile16_rows_per_s"]
+
     gc["pass_rows_per_s"] = rows_pass / (kavg * 1e-3)
-    gc["pass_over_ceiling"] = gc["pass_rows_per_s"] / gc["rows_per_s"]
-    gc["note"] = ("f3s_probe_gather: uniformly random K and V rows of 128 B (head 0), the pass's "
-                  "load shape, on the workload's tensors; the pass's rows are its gathered K and "
-                  "V rows per head (masked: attended columns; tile-dense: 16 per tile)")
+    gc["pass_over_ceiling"] = gc["pass_rows_per_s"] / ceiling(masked)
+    gc["note"] = ("f3s_probe_gather, the pass's load shape (K and V rows of 128 B, head 0) on the "
+                  "workload's tensors: rows_per_s over uniformly random rows (a masked pass's "
+                  "columns), tile16_rows_per_s over runs of 16 consecutive rows (a tile-dense "
+                  "pass's tiles), stream_rows_per_s over rows in order; pass_over_ceiling divides "
+                  "the pass's gathered K and V rows per head (masked: attended columns; "
+                  "tile-dense: 16 per tile) per second by the ceiling of its semantics")
     res["gather_ceiling"] = gc
 
     if not args.no_reference_launches:
@@ -558,7 +584,7 @@ def main() -> int:
                           "passes": reps, "compulsory_bytes": b,
                           "roofline_frac": b / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS,
                           "gathered_rows_per_s": rows / (mean * 1e-3),
-                          "over_gather_ceiling": rows / (mean * 1e-3) / gc["rows_per_s"]}
+                          "over_gather_ceiling": rows / (mean * 1e-3) / ceiling(sem_masked)}
 
         leg("tile_dense_planned",
             lambda: ref_plan.forward(dQ, dK, dV, dO, masked=False, stream=stream),
