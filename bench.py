@@ -333,9 +333,18 @@ def main() -> int:
             f3s.synchronize()
             times.append(e0.elapsed_ms(e1))
         best = min(times)
+        # and a plain fill of the same buffer (f3s_memset): the write-only rate
+        fills = []
+        for _ in range(args.steps):
+            e0.record()
+            dst.fill_bytes(0x5A)
+            e1.record()
+            f3s.synchronize()
+            fills.append(e0.elapsed_ms(e1))
         # read + write bytes over the fastest copy: the practical HBM rate
         print(json.dumps({"copy_probe_bytes": nb, "launches": args.steps,
-                          "copy_ms": times, "copy_GBps_rw": 2 * nb / best / 1e6}), flush=True)
+                          "copy_ms": times, "copy_GBps_rw": 2 * nb / best / 1e6,
+                          "fill_ms": fills, "fill_GBps_w": nb / min(fills) / 1e6}), flush=True)
         return 0
     if args.gather_probe:
         # uniformly random 128-byte K and V rows, the config-4 pass's column
