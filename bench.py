@@ -206,6 +206,48 @@ def gather_ceiling(f3s, dK, dV, rows: int, H: int, count: int, stream, reps: int
             "table_bytes_each": rows * stride, "pattern": pattern}
 
 
+def host_handover(f3s, rp, ci, Q, K, V, n: int, H: int, d: int, masked: bool,
+                  reps: int = 3) -> dict:
+    """The reference harness's flow from host memory, PCIe copies included
+    (tests/test_fused_3s_v2.cu:66-137): the drop-in converter
+    (convert_csr_to_block_sparse: host CSR in, host tile lists and masks
+    out), the host window order (generate_balanced_window_order), then one
+    pass from host buffers -- tile lists, order and Q/K/V uploaded, the
+    drop-in launch in that order, O downloaded.  Host wall time of each step,
+    the best of `reps`; pageable host memory, as the harness uses."""
+    conv, ordt, pas = [], [], []
+    for _ in range(reps):
+        f3s.synchronize()
+        t0 = time.perf_counter()
+        fmt = f3s.convert_csr_to_block_sparse(n, rp, ci, verbose=False)
+        t1 = time.perf_counter()
+        host_order = f3s.generate_balanced_window_order(fmt)
+        t2 = time.perf_counter()
+        offs = f3s.DeviceArray.from_numpy(np.ascontiguousarray(fmt.window_offsets, np.int32))
+        cols = f3s.DeviceArray.from_numpy(np.ascontiguousarray(fmt.block_col_indices, np.int32))
+        mask = (f3s.DeviceArray.from_numpy(np.ascontiguousarray(fmt.tile_masks, np.uint16))
+                if masked else None)
+        dord = f3s.DeviceArray.from_numpy(host_order)
+        dbsf = f3s.DeviceBSF(n, int(fmt.num_row_windows), len(fmt.block_col_indices), offs, cols,
+                             mask)
+        dq, dk, dv = (f3s.DeviceArray.from_numpy(x.view(np.uint16)) for x in (Q, K, V))
+        do = f3s.DeviceArray((n, H, d), np.float32)
+        f3s.attention_fwd(dq, dk, dv, do, dbsf, dord, masked=masked, H=H, d=d)
+        out = do.numpy()
+        t3 = time.perf_counter()
+        conv.append(t1 - t0)
+        ordt.append(t2 - t1)
+        pas.append(t3 - t2)
+        del fmt, host_order, offs, cols, mask, dord, dbsf, dq, dk, dv, do, out
+    edges = int(rp[n])
+    total = min(conv) + min(ordt) + min(pas)
+    return {"convert_us": min(conv) * 1e6, "order_us": min(ordt) * 1e6,
+            "pass_us": min(pas) * 1e6, "total_us": total * 1e6, "edges_per_s": edges / total,
+            "note": "host buffers in and out (PCIe copies included): convert_csr_to_block_sparse, "
+                    "generate_balanced_window_order, then upload of tile lists, order and Q/K/V, "
+                    "the drop-in launch and O back; never the headline value"}
+
+
 def host_cpu_model() -> str:
     """The host CPU's model name (first processor of /proc/cpuinfo)."""
     try:
@@ -298,8 +340,8 @@ def main() -> int:
                     help="time the drop-in launch f3s_attention_fwd (each window whole, in "
                          "the given order; the reference's launch) instead of a plan")
     ap.add_argument("--no-reference-launches", action="store_true",
-                    help="skip timing the reference's semantics and launch shape after the "
-                         "timed region")
+                    help="skip timing the reference's semantics and launch shape, and the "
+                         "flow from host memory, after the timed region")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--gather-probe", action="store_true",
                     help="only measure the random-gather ceiling (f3s_probe_gather) over "
@@ -608,6 +650,10 @@ def main() -> int:
                                       stream=stream),
             True, "unplanned", reps_m)
         res["reference_launches"] = legs
+
+    if not args.no_reference_launches:
+        print("[bench] timing the flow from host memory ...", file=sys.stderr, flush=True)
+        res["host_handover"] = host_handover(f3s, rp, ci, Q, K, V, n, H, d, masked)
 
     if not args.no_cpu_baseline:
         print("[bench] timing the reference CPU baseline ...", file=sys.stderr, flush=True)
