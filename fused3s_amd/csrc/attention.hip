@@ -1169,6 +1169,11 @@ static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const
     // The schedule's scratch: returned to the allocator in stream order when
     // this function returns, i.e. after the last launch that reads it.
     StreamBuffer scratch(st);
+    // A window holds at most one tile per block column, W of them, so with
+    // W <= kHeavyMinTiles no window of a valid block-sparse form is heavy:
+    // then no team launch (the schedule gets an empty team list, so any
+    // window still runs on one wave).
+    const bool heavy_possible = W > kHeavyMinTiles;
     if (p.team == 1 && !wide_features(n, H) && W > kHeavyMaxWindows &&
         (!ordered || (int64_t)W * H >= kSchedOrderedMin)) {
         // the library's schedule (see sched_fill): heavy windows on teams of
@@ -1179,19 +1184,21 @@ static f3s_status attention_fwd_impl(const uint16_t* Q, const uint16_t* K, const
             sp = static_cast<char*>(scratch.ptr);
         }
         int32_t *team = nullptr, *sched = nullptr;
-        F3S_TRY(launch_schedule(d_window_offsets, d_window_order, W, kHeavyMaxWindows, sp, st,
-                                &team, &sched));
+        F3S_TRY(launch_schedule(d_window_offsets, d_window_order, W,
+                                heavy_possible ? kHeavyMaxWindows : 0, sp, st, &team, &sched));
         const int64_t L = sched_xcd_slots(W);
-        AttnParams ph = p;
-        ph.window_order = team;
-        ph.xcd_contiguous = 0;
-        ph.team = kTeamLarge;
-        ph.num_items = (int64_t)kHeavyMaxWindows * kTeamLarge;
-        F3S_TRY(launch(ph, H, scale, st));
+        if (heavy_possible) {
+            AttnParams ph = p;
+            ph.window_order = team;
+            ph.xcd_contiguous = 0;
+            ph.team = kTeamLarge;
+            ph.num_items = (int64_t)kHeavyMaxWindows * kTeamLarge;
+            F3S_TRY(launch(ph, H, scale, st));
+        }
         p.window_order = sched;
         p.xcd_contiguous = 0;
         p.num_items = kXcds * L;
-    } else if (p.team == 1 && ordered && !wide_features(n, H)) {
+    } else if (p.team == 1 && ordered && !wide_features(n, H) && heavy_possible) {
         // The order's sequence: teams of 16 waves for the heavy windows among
         // its first kHeavyMaxWindows entries (the reference's descending order
         // puts the hubs there), then one wave per entry for all others; each

@@ -643,6 +643,25 @@ def test_unplanned_heavy_windows(gpu):
         assert np.array_equal(got_by["natural"].view(np.uint32), got_by["sorted"].view(np.uint32))
 
 
+@pytest.mark.parametrize("H", [2, 4])
+def test_unplanned_schedule_without_heavy_windows(gpu, H):
+    # 800 windows: past the 512 from which the drop-in launch runs its
+    # schedule, but no window can hold more than 800 tiles (one per block
+    # column), under the 1,024 a heavy window needs, so the launch skips the
+    # team launch; given an order, one wave per entry.  Every window runs
+    # whole on one wave either way: same bits, within the oracle's bar.
+    rp, ci = random_csr(16 * 800, 6, 71, self_loops=True)
+    p = Problem(gpu, rp, ci, H=H, normal=True, seed=71)
+    assert p.bsf.W == 800
+    order = gpu.window_order_device(p.bsf)
+    for masked in (True, False):
+        want = p.oracle(masked, scale=0.125)
+        nat = p.run(masked, scale=0.125)
+        srt = p.run(masked, order=order, scale=0.125)
+        assert_close(nat, want, f"no heavy windows, natural order, H={H} masked={masked}")
+        assert np.array_equal(nat.view(np.uint32), srt.view(np.uint32)), (H, masked)
+
+
 def test_unplanned_schedule_names_windows(gpu):
     # From 2^18 window-heads on (plans and the drop-in launch alike), a window
     # order only names the windows to compute, and the library's schedule
