@@ -206,6 +206,42 @@ def gather_ceiling(f3s, dK, dV, rows: int, H: int, count: int, stream, reps: int
             "table_bytes_each": rows * stride, "pattern": pattern}
 
 
+def tile_dense_oracle(Q, K, V, offs: np.ndarray, bcol: np.ndarray, n: int, H: int, d: int,
+                      budget_tiles: int = 400_000) -> dict | None:
+    """The TILE_DENSE truth (tests/test_fused_3s_v2.cu:17-59, restated in
+    oracle/f3s_oracle.c) timed on the host cores this process may use (at
+    most 16), over the first windows holding about `budget_tiles` tiles (a
+    bounded sample: the whole of config 4 is ~1 TFLOP of tile work).  An
+    oracle, not the baseline."""
+    lib_path = ROOT / "oracle" / "liboracle.so"
+    if not lib_path.exists():
+        return None
+    lib = C.CDLL(str(lib_path))
+    fn = lib.orc_tile_dense_attention
+    fn.restype = None
+    fn.argtypes = ([C.c_int32] * 3 + [C.c_void_p] * 5 + [C.c_float, C.c_int32, C.c_int32,
+                                                         C.c_void_p, C.c_int32])
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    offs = np.ascontiguousarray(offs, np.int32)
+    bcol = np.ascontiguousarray(bcol if len(bcol) else np.zeros(1, np.int32), np.int32)
+    W = len(offs) - 1
+    w1 = int(min(W, np.searchsorted(offs, budget_tiles, side="right")))
+    w1 = max(w1, 1)
+    r1 = min(n, 16 * w1)
+    tiles = int(offs[w1] - offs[0])
+    Qf, Kf, Vf = (np.ascontiguousarray(x.reshape(n, H, d), np.float32) for x in (Q, K, V))
+    O = np.zeros((n, H, d), np.float32)
+    t0 = time.perf_counter()
+    fn(n, d, H, Qf.ctypes.data, Kf.ctypes.data, Vf.ctypes.data, offs.ctypes.data,
+       bcol.ctypes.data, 1.0, 0, r1, O.ctypes.data, threads)
+    dt = time.perf_counter() - t0
+    total = int(offs[-1])
+    return {"tiles_per_s": tiles * H / dt, "threads": threads, "cpu_model": host_cpu_model(),
+            "sample": f"windows 0..{w1 - 1} ({tiles} of {total} tiles) x {H} head(s), "
+                      f"{dt:.2f} s on {threads} threads (OpenMP)",
+            "full_graph_s_estimate": dt * total / max(tiles, 1)}
+
+
 def host_handover(f3s, rp, ci, Q, K, V, n: int, H: int, d: int, masked: bool,
                   reps: int = 3) -> dict:
     """The reference harness's flow from host memory, PCIe copies included
@@ -662,6 +698,9 @@ def main() -> int:
         print("[bench] timing the CPU restatement on all available cores ...", file=sys.stderr,
               flush=True)
         res["cpu_baseline_all_cores"] = cpu_baseline_all_cores(rp, ci, Q, K, V, n, H, d)
+        print("[bench] timing the tile-dense oracle on a sample ...", file=sys.stderr, flush=True)
+        res["tile_dense_oracle"] = tile_dense_oracle(Q, K, V, bsf.window_offsets.numpy(),
+                                                     bsf.block_col.numpy(), n, H, d)
     print(json.dumps(res), flush=True)
     return 0
 
