@@ -802,6 +802,36 @@ def test_window_order_with_invalid_entries(gpu, H):
             assert_close(got[rows], want[rows], what)
 
 
+@pytest.mark.parametrize("n", [0, 37, 16 * 600])
+def test_edgeless_graphs(gpu, n):
+    # No edges (and, for n = 0, no nodes): no tiles, and every row of O is
+    # exactly 0 in both semantics, through every launch shape -- 600 windows
+    # take the drop-in launch's schedule with every window in its lightest
+    # class.
+    from fused3s_amd import _lib
+    rp, ci = np.zeros(n + 1, np.int32), np.zeros(0, np.int32)
+    p = Problem(gpu, rp, ci, H=2, seed=5)
+    bsf = p.bsf
+    assert bsf.T == 0 and bsf.W == (n + 15) // 16
+    offs, _, _ = orc.convert(n, rp, ci)
+    assert np.array_equal(p.host_bsf().window_offsets, offs)
+    order = gpu.window_order_device(bsf) if bsf.W else None
+    for masked in (True, False):
+        runs = {"natural": p.run(masked), "ordered": p.run(masked, order=order)}
+        for planned, compiled in ((True, False), (True, True)):
+            if compiled and not masked:
+                continue
+            runs[f"plan compiled={compiled}"] = p.run(masked, planned=True, compiled=compiled)
+        p.dO.fill_bytes(0xFF)
+        assert _lib.hip().f3s_attention_fwd_noalloc(
+            p.dQ.ptr, p.dK.ptr, p.dV.ptr, p.dO.ptr, bsf.window_offsets.ptr, bsf.block_col.ptr,
+            bsf.tile_mask.ptr if masked else None, None, bsf.W, n, 64, 2, 1.0, None) == 0
+        gpu.synchronize()
+        runs["noalloc"] = p.dO.numpy()
+        for what, got in runs.items():
+            assert got.shape == (n, 2, 64) and not np.any(got), (n, masked, what)
+
+
 def test_attention_rejects_bad_args(gpu):
     rp, ci = random_csr(40, 3, 1)
     p = Problem(gpu, rp, ci)
