@@ -199,6 +199,32 @@ def test_converter_hub_windows(gpu):
     check_converter(gpu, rp, ci)
 
 
+def test_converter_edge_count_boundaries(gpu):
+    # Windows at each edge-count boundary of the converter: the persistent
+    # kernel takes up to 1,024 edges per window (256 threads x 4), the hub
+    # kernel keeps up to 8,192 in registers (1,024 threads x 8) and ORs the
+    # masks of heavier windows straight into the output; one window of each
+    # of 1,023 / 1,024 / 1,025 / 8,191 / 8,192 / 8,193 edges (row 0 of the
+    # window carries the excess, partly repeated columns), beside light ones.
+    n = 16 * 64
+    r = rng(12)
+    rows, cols = [np.arange(n)], [np.arange(n)]                 # self-loops
+    for k, E in enumerate((1023, 1024, 1025, 8191, 8192, 8193)):
+        u = 16 * (8 * k + 3)
+        extra = E - 16                                           # the window's 16 self-loops
+        rows.append(np.full(extra, u))
+        cols.append(r.integers(0, n, extra))                     # repeats included
+    rr, cc = np.concatenate(rows), np.concatenate(cols)
+    order = np.lexsort((cc, rr))
+    rr, cc = rr[order], cc[order]
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, rr + 1, 1)
+    rp = np.cumsum(rp).astype(np.int32)
+    edges = np.diff(rp[::16])
+    assert [int(edges[8 * k + 3]) for k in range(6)] == [1023, 1024, 1025, 8191, 8192, 8193]
+    check_converter(gpu, rp, cc.astype(np.int32))
+
+
 def test_converter_column_slices(gpu):
     # 137,500 block columns: one 4,297-word bitmap in the persistent kernel
     # (more than the per-window kernel's 65,536-column slice), windows with
