@@ -828,6 +828,37 @@ def test_window_order_with_invalid_entries(gpu, H):
             assert_close(got[rows], want[rows], what)
 
 
+def test_attention_chunk_boundaries(gpu):
+    # Masked passes take a window's attended columns 32 at a time, tile-dense
+    # ones its tiles two at a time: windows attending exactly 1, 31, 32, 33,
+    # 63, 64, 65, 96, 97, 128 and 129 distinct columns (spread over their 16
+    # rows), and so holding from 1 to dozens of tiles, odd and even, against
+    # the oracle in both semantics and every launch shape.
+    sizes = (1, 31, 32, 33, 63, 64, 65, 96, 97, 128, 129)
+    W = 2 * len(sizes)
+    n = 16 * W
+    r = rng(13)
+    rows, cols = [], []
+    for k, sz in enumerate(sizes):
+        w = 2 * k                                        # windows 0, 2, 4, ...; odd ones empty
+        c = r.choice(n, sz, replace=False)
+        rows.append(16 * w + (np.arange(sz) % 16))
+        cols.append(c)
+    rr, cc = np.concatenate(rows), np.concatenate(cols)
+    o = np.lexsort((cc, rr))
+    rr, cc = rr[o], cc[o]
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, rr + 1, 1)
+    rp = np.cumsum(rp).astype(np.int32)
+    p = Problem(gpu, rp, cc.astype(np.int32), H=2, normal=True, seed=13)
+    for masked in (True, False):
+        want = p.oracle(masked, scale=0.125)
+        for planned, compiled in ((False, False), (True, False), (True, True)):
+            got = p.run(masked, planned=planned, seg=0, scale=0.125, compiled=compiled and masked)
+            assert_close(got, want, f"chunk boundaries masked={masked} planned={planned} "
+                                    f"compiled={compiled}")
+
+
 @pytest.mark.parametrize("n", [0, 37, 16 * 600])
 def test_edgeless_graphs(gpu, n):
     # No edges (and, for n = 0, no nodes): no tiles, and every row of O is
