@@ -467,6 +467,29 @@ def test_attention_closed_forms(gpu):
         assert np.allclose(got[16 * w:16 * w + 16], want, atol=1e-3)
 
 
+def test_attention_wide_logit_range(gpu):
+    # Q and K drawn with standard deviation 4 (logits of standard deviation
+    # ~128, most rows' softmax close to one-hot; the running max moves by
+    # hundreds between chunks) and a scale of 0 (every weight equal: O is the
+    # plain mean of V over the attended columns), against the oracle, every
+    # launch shape, both semantics.
+    rp, ci = random_csr(2000, 24, 14, self_loops=True)
+    p = Problem(gpu, rp, ci, H=2, normal=True, seed=14)
+    r = rng(15)
+    for a, d in ((p.Q, p.dQ), (p.K, p.dK)):
+        a[:] = (r.standard_normal(a.shape) * 4).astype(np.float16)
+        d.upload(a.view(np.uint16))
+    p.Qf, p.Kf = p.Q.astype(np.float32), p.K.astype(np.float32)
+    for scale in (1.0, 0.0):
+        for masked in (True, False):
+            want = p.oracle(masked, scale=scale)
+            for planned, compiled in ((False, False), (True, False), (True, True)):
+                got = p.run(masked, planned=planned, seg=4, scale=scale,
+                            compiled=compiled and masked)
+                assert_close(got, want, f"wide logits scale={scale} masked={masked} "
+                                        f"planned={planned} compiled={compiled}")
+
+
 def test_attention_deterministic(gpu):
     rp, ci = star_graph(5000, hubs=(1,))
     p = Problem(gpu, rp, ci, normal=True, seed=4)
