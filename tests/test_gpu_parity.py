@@ -490,6 +490,37 @@ def test_attention_wide_logit_range(gpu):
                                         f"planned={planned} compiled={compiled}")
 
 
+def test_padded_buffers_with_nan_padding(gpu):
+    # The reference's buffers have 16W rows, padded (tests/test_fused_3s_v2.cu:
+    # 93-120).  Given such buffers whose padding rows hold NaN, the pass
+    # reads none of them (loads past n rows return 0; padded columns are
+    # excluded, as on the reference's CPU side) and writes none: rows < n
+    # match the oracle, rows >= n keep what they held.
+    n = 16 * 50 + 5
+    W = (n + 15) // 16
+    rp, ci = random_csr(n, 10, 16, self_loops=True)
+    p = Problem(gpu, rp, ci, H=2, normal=True, seed=16)
+    nan16 = np.full((16 * W - n, 2, 64), 0x7E00, np.uint16)
+    pads = [gpu.DeviceArray.from_numpy(np.concatenate([a.view(np.uint16), nan16]))
+            for a in (p.Q, p.K, p.V)]
+    dO = gpu.DeviceArray((16 * W, 2, 64), np.float32)
+    for masked in (True, False):
+        want = p.oracle(masked, scale=0.125)
+        runs = {
+            "drop-in": lambda: gpu.attention_fwd(*pads, dO, p.bsf, None, masked=masked, H=2,
+                                                 scale=0.125),
+            "plan": lambda: gpu.Plan(p.bsf, None, H=2).forward(*pads, dO, masked=masked,
+                                                               scale=0.125),
+        }
+        for what, fn in runs.items():
+            dO.fill_bytes(0xFF)
+            fn()
+            gpu.synchronize()
+            got = dO.numpy()
+            assert_close(got[:n], want, f"padded buffers, {what}, masked={masked}")
+            assert np.all(got[n:].view(np.uint32) == 0xFFFFFFFF), (what, masked)
+
+
 def test_attention_deterministic(gpu):
     rp, ci = star_graph(5000, hubs=(1,))
     p = Problem(gpu, rp, ci, normal=True, seed=4)
