@@ -148,8 +148,10 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * slot by slot across the XCDs (longest windows first for the tail, each
  * share's contiguous windows on one or a few XCDs for the L2; on a
  * community-ordered graph the reference's descending order would scatter
- * each community over the whole run).  Four small kernels (~30 us)
- * build the schedule in scratch of about 9 bytes per window taken from the
+ * each community over the whole run).  With W <= 1024 no window can be heavy
+ * (one tile per block column at most) and no team launch is made.  Three
+ * small kernels (four given an order; ~15-30 us) build the schedule in
+ * scratch of about 9 bytes per window taken from the
  * library's pool and returned to it in stream order on `stream` (the call
  * does not wait).  Tensors past ~4 GiB take the sequence of the order, as
  * small graphs do.  Every other path allocates nothing. */
