@@ -639,6 +639,12 @@ def main() -> int:
 
     gc["pass_rows_per_s"] = rows_pass / (kavg * 1e-3)
     gc["pass_over_ceiling"] = gc["pass_rows_per_s"] / ceiling(masked)
+    if res.get("below_l2") and H == 1:
+        # the traffic below the L2 (reads and writes, from the committed
+        # profile) against the rate at which the same loads read rows in
+        # order (with one head the rows are contiguous)
+        stream_gbs = gc["stream_rows_per_s"] * 128 / 1e9
+        res["below_l2"]["frac_of_in_order_read_rate"] = res["below_l2"]["GBps"] / stream_gbs
     gc["note"] = ("f3s_probe_gather, the pass's load shape (K and V rows of 128 B, head 0) on the "
                   "workload's tensors: rows_per_s over uniformly random rows (a masked pass's "
                   "columns), tile16_rows_per_s over runs of 16 consecutive rows (a tile-dense "
