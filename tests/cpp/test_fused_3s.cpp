@@ -11,7 +11,8 @@
 // 1e-2; the exit code is non-zero on failure.
 //
 //   test_fused_3s [dataset_dir] [--semantics masked|tile_dense] [--reps R]
-//                 [--config N]   (synthetic config 1-3 instead of a directory)
+//                 [--config N]   (synthetic config 1-5 instead of a directory; configs
+//                 4 and 5 with their N(0,1) features, at one head as the reference)
 //                 [--zero-columns]  (every column index read as 0: the graph the
 //                 reference's as-shipped loader produces, include/utils.cuh:36,
 //                 on which its published kernel times were measured)
@@ -27,6 +28,7 @@
 #include <chrono>
 #include <iostream>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "f3s/graph.hpp"
@@ -56,6 +58,12 @@ GraphData synthetic(int cfg)
     } else if (cfg == 3) {
         n = 3327;
         rc = f3s_gen_powerlaw(n, 9104, 2.8, 99, 1, 1, 43, &rp, &ci, &nnz);
+    } else if (cfg == 4) {
+        n = 1000000;
+        rc = f3s_gen_powerlaw(n, 16000000, 2.2, 16384, 1, 1, 44, &rp, &ci, &nnz);
+    } else if (cfg == 5) {
+        n = 2400000;
+        rc = f3s_gen_sbm(n, 4096, 50.0, 0.8, 1, 45, &rp, &ci, &nnz);
     }
     if (rc != 0) {
         std::cerr << "cannot generate config " << cfg << ": " << f3s_host_last_error() << std::endl;
@@ -147,10 +155,11 @@ int main(int argc, char** argv)
     // Seeded fp16 inputs; the CPU truth widens the same fp16 values.
     const size_t feat = (size_t)n * feat_dim;
     std::vector<uint16_t> hQ(feat), hK(feat), hV(feat);
-    const int dist = 0;   // U[-1, 1)
-    if (f3s_gen_features_f16(42, 0, (int64_t)feat, dist, hQ.data()) ||
-        f3s_gen_features_f16(42, 1, (int64_t)feat, dist, hK.data()) ||
-        f3s_gen_features_f16(42, 2, (int64_t)feat, dist, hV.data())) {
+    const int dist = cfg >= 4 ? 1 : 0;                  // N(0, 1) for configs 4, 5; else U[-1, 1)
+    const uint64_t seed = cfg >= 4 ? (uint64_t)(40 + cfg) : 42;
+    if (f3s_gen_features_f16(seed, 0, (int64_t)feat, dist, hQ.data()) ||
+        f3s_gen_features_f16(seed, 1, (int64_t)feat, dist, hK.data()) ||
+        f3s_gen_features_f16(seed, 2, (int64_t)feat, dist, hV.data())) {
         std::cerr << "FAILURE: feature generation" << std::endl;
         return 1;
     }
@@ -159,14 +168,16 @@ int main(int argc, char** argv)
     orc_cast_f16_to_f32(hK.data(), fK.data(), (int64_t)feat);
     orc_cast_f16_to_f32(hV.data(), fV.data(), (int64_t)feat);
 
-    std::cout << "Computing CPU ground truth..." << std::endl;
+    // the truth on the host's cores (at most 16, a one-GPU box's share)
+    const int threads = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::cout << "Computing CPU ground truth (" << threads << " threads)..." << std::endl;
     if (masked)
         orc_masked_attention(n, feat_dim, 1, fQ.data(), fK.data(), fV.data(), graph.row_ptr.data(),
-                             graph.col_ind.data(), 1.0f, 0, n, O_cpu.data(), 8);
+                             graph.col_ind.data(), 1.0f, 0, n, O_cpu.data(), threads);
     else
         orc_tile_dense_attention(n, feat_dim, 1, fQ.data(), fK.data(), fV.data(),
                                  format.window_offsets.data(), format.block_col_indices.data(),
-                                 1.0f, 0, n, O_cpu.data(), 8);
+                                 1.0f, 0, n, O_cpu.data(), threads);
 
     Dev dQ(2 * feat), dK(2 * feat), dV(2 * feat), dO(4 * feat);
     Dev dOffs(4 * (W + 1)), dBcol(4 * (T > 0 ? T : 1)), dMask(32 * (T > 0 ? T : 1)), dOrder(4 * (W > 0 ? W : 1));

@@ -27,6 +27,19 @@ def test_harness(gpu, args):
     assert "SUCCESS" in r.stdout and "bit-exact" in r.stdout
 
 
+@pytest.mark.slow
+@pytest.mark.parametrize("cfg", ["4", "5"])
+def test_harness_large_configs(gpu, cfg):
+    # the reference's flow at the large configurations (one head, masked):
+    # the converter bit-exact against the CPU restatement and every output
+    # row against the CPU truth
+    r = subprocess.run([str(EXE), "--config", cfg, "--reps", "10"], capture_output=True,
+                       text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0, r.stderr
+    assert "SUCCESS" in r.stdout and "bit-exact" in r.stdout
+
+
 def test_harness_binary_graph_file(gpu, tmp_path):
     # text dataset -> binary graph file (with the GPU converter's block-sparse
     # form) -> the harness again, reading the binary file
