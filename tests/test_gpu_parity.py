@@ -952,6 +952,25 @@ def test_attention_rejects_bad_args(gpu):
     with pytest.raises(gpu.F3SError) as e:
         gpu.attention_fwd(p.dQ, p.dK, p.dV, p.dO, p.bsf, H=65)
     assert e.value.name == "F3S_EUNSUPPORTED"
+    # through the C-ABI: W that does not match n, a feature pointer off its
+    # 16-byte alignment, a misaligned mask pointer, a NULL block list -- each
+    # an F3S_EINVAL before any launch, with the output untouched
+    from fused3s_amd import _lib
+    lib = _lib.hip()
+    b = p.bsf
+    args = dict(Q=p.dQ.ptr, K=p.dK.ptr, V=p.dV.ptr, O=p.dO.ptr, offs=b.window_offsets.ptr,
+                cols=b.block_col.ptr, mask=b.tile_mask.ptr, order=None, W=b.W, n=p.n)
+    bad = [dict(W=b.W + 1), dict(Q=p.dQ.ptr + 2), dict(O=p.dO.ptr + 4),
+           dict(mask=b.tile_mask.ptr + 2), dict(cols=None)]
+    for change in bad:
+        a = {**args, **change}
+        p.dO.fill_bytes(0x7F)
+        for fn in (lib.f3s_attention_fwd, lib.f3s_attention_fwd_noalloc):
+            st = fn(a["Q"], a["K"], a["V"], a["O"], a["offs"], a["cols"], a["mask"], a["order"],
+                    a["W"], a["n"], 64, 1, 1.0, None)
+            assert st == 1, (change, fn.__name__, st, lib.f3s_last_error())
+        gpu.synchronize()
+        assert np.all(p.dO.numpy().view(np.uint32) == 0x7F7F7F7F), change
 
 
 # ------------------------------------------------------ naive comparator
