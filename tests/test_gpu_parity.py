@@ -973,6 +973,30 @@ def test_attention_rejects_bad_args(gpu):
         assert np.all(p.dO.numpy().view(np.uint32) == 0x7F7F7F7F), change
 
 
+def test_plan_rejects_bad_args(gpu):
+    # a plan's pass with another head count or another n, and a compile
+    # without masks or with a misaligned mask pointer: F3S_EINVAL, O untouched
+    from fused3s_amd import _lib
+    lib = _lib.hip()
+    rp, ci = random_csr(200, 5, 17)
+    p = Problem(gpu, rp, ci, H=2, seed=17)
+    plan = gpu.Plan(p.bsf, None, H=2)
+    b = p.bsf
+    p.dO.fill_bytes(0x7F)
+    for H, n in ((1, p.n), (2, p.n + 16)):
+        st = lib.f3s_attention_fwd_planned(plan.handle, p.dQ.ptr, p.dK.ptr, p.dV.ptr, p.dO.ptr,
+                                           b.block_col.ptr, b.tile_mask.ptr, n, 64, H, 1.0, None)
+        assert st == 1, (H, n, lib.f3s_last_error())
+    for mask in (None, b.tile_mask.ptr + 2):
+        st = lib.f3s_plan_compile(plan.handle, b.block_col.ptr, mask, p.n, None)
+        assert st == 1, lib.f3s_last_error()
+    gpu.synchronize()
+    assert np.all(p.dO.numpy().view(np.uint32) == 0x7F7F7F7F)
+    # and the plan still works after the rejected calls
+    got = p.run(True, planned=True, compiled=True)
+    assert_close(got, p.oracle(True), "plan after rejected calls")
+
+
 # ------------------------------------------------------ naive comparator
 
 @pytest.mark.parametrize("case", ["cora", "random", "multigraph"])
