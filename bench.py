@@ -206,42 +206,6 @@ def gather_ceiling(f3s, dK, dV, rows: int, H: int, count: int, stream, reps: int
             "table_bytes_each": rows * stride, "pattern": pattern}
 
 
-def tile_dense_oracle(Q, K, V, offs: np.ndarray, bcol: np.ndarray, n: int, H: int, d: int,
-                      budget_tiles: int = 400_000) -> dict | None:
-    """The TILE_DENSE truth (tests/test_fused_3s_v2.cu:17-59, restated in
-    oracle/f3s_oracle.c) timed on the host cores this process may use (at
-    most 16), over the first windows holding about `budget_tiles` tiles (a
-    bounded sample: the whole of config 4 is ~1 TFLOP of tile work).  An
-    oracle, not the baseline."""
-    lib_path = ROOT / "oracle" / "liboracle.so"
-    if not lib_path.exists():
-        return None
-    lib = C.CDLL(str(lib_path))
-    fn = lib.orc_tile_dense_attention
-    fn.restype = None
-    fn.argtypes = ([C.c_int32] * 3 + [C.c_void_p] * 5 + [C.c_float, C.c_int32, C.c_int32,
-                                                         C.c_void_p, C.c_int32])
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    offs = np.ascontiguousarray(offs, np.int32)
-    bcol = np.ascontiguousarray(bcol if len(bcol) else np.zeros(1, np.int32), np.int32)
-    W = len(offs) - 1
-    w1 = int(min(W, np.searchsorted(offs, budget_tiles, side="right")))
-    w1 = max(w1, 1)
-    r1 = min(n, 16 * w1)
-    tiles = int(offs[w1] - offs[0])
-    Qf, Kf, Vf = (np.ascontiguousarray(x.reshape(n, H, d), np.float32) for x in (Q, K, V))
-    O = np.zeros((n, H, d), np.float32)
-    t0 = time.perf_counter()
-    fn(n, d, H, Qf.ctypes.data, Kf.ctypes.data, Vf.ctypes.data, offs.ctypes.data,
-       bcol.ctypes.data, 1.0, 0, r1, O.ctypes.data, threads)
-    dt = time.perf_counter() - t0
-    total = int(offs[-1])
-    return {"tiles_per_s": tiles * H / dt, "threads": threads, "cpu_model": host_cpu_model(),
-            "sample": f"windows 0..{w1 - 1} ({tiles} of {total} tiles) x {H} head(s), "
-                      f"{dt:.2f} s on {threads} threads (OpenMP)",
-            "full_graph_s_estimate": dt * total / max(tiles, 1)}
-
-
 def host_handover(f3s, rp, ci, Q, K, V, n: int, H: int, d: int, masked: bool,
                   reps: int = 3) -> dict:
     """The reference harness's flow from host memory, PCIe copies included
@@ -296,58 +260,235 @@ def host_cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(rp, ci, Q, K, V, n: int, d: int) -> dict | None:
-    """The reference's cpu_sparse_attention_csr (single thread) over the
-    whole graph, on this host."""
+ABS_TOL, REL_TOL = 2e-3, 1e-2   # the north star's bounds against the fp32 CPU truth
+
+# Sources each profiled kernel is compiled from: a committed profile records
+# their digest, and the bench flags a profile whose digest differs from the
+# sources it runs.
+KERNEL_SOURCES = {
+    "fused_attention": ["fused3s_amd/csrc/attention.hip", "fused3s_amd/csrc/attn_common.hpp",
+                        "fused3s_amd/csrc/attn_plan.hpp", "fused3s_amd/csrc/f3s_common.hpp",
+                        "fused3s_amd/csrc/f3s_device.hpp"],
+    "converter": ["fused3s_amd/csrc/convert.hip", "fused3s_amd/csrc/f3s_common.hpp",
+                  "fused3s_amd/csrc/f3s_device.hpp"],
+}
+
+
+def source_digest(kernel: str) -> str:
+    """First 16 hex digits of the SHA-256 over the named kernel's source
+    files (path and bytes, in list order)."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES[kernel]:
+        h.update(rel.encode() + b"\0")
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def read_profile_field(path: Path, key: str) -> str | None:
+    """`key value` line of a committed profile, the value as text."""
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split(None, 1)
+        if len(parts) == 2 and parts[0] == key:
+            return parts[1].strip()
+    return None
+
+
+def oracle_module():
+    """The CPU oracle's ctypes view (tests/_oracle.py over oracle/liboracle.so):
+    the checker of the CPU leg, never what is timed as the GPU path."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import _oracle
+    return _oracle
+
+
+def check_threads() -> int:
+    """Host threads the checker and the all-core baseline use: the cores this
+    process may run on, at most 16 (a one-GPU box's CPU share)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def compare_rows(got: np.ndarray, want: np.ndarray) -> dict:
+    """Every element of a pass's output against the fp32 truth: max abs error,
+    normwise max rel error (max abs / max |truth|), the largest elementwise
+    relative error over |truth| >= 0.1 (for information), and whether the
+    output is within the north star's bounds with no NaN or inf."""
+    g = got.reshape(-1)
+    w = want.reshape(-1)
+    assert g.size == w.size, (got.shape, want.shape)
+    max_abs = 0.0
+    max_ref = 0.0
+    rel_elem = 0.0
+    bad = 0
+    step = 1 << 22
+    for i in range(0, g.size, step):
+        gi, wi = g[i:i + step], w[i:i + step]
+        fin = np.isfinite(gi)
+        bad += int(gi.size - np.count_nonzero(fin))
+        diff = np.abs(gi - wi)
+        if diff.size:
+            max_abs = max(max_abs, float(np.max(diff, where=fin, initial=0.0)))
+            aw = np.abs(wi)
+            max_ref = max(max_ref, float(aw.max()))
+            big = aw >= 0.1
+            if np.any(big):
+                rel_elem = max(rel_elem, float((diff[big] / aw[big]).max()))
+    max_rel = max_abs / max_ref if max_ref > 0 else (0.0 if max_abs == 0 else float("inf"))
+    return {"max_abs": max_abs, "max_rel": max_rel, "max_rel_elem_ge_0.1": rel_elem,
+            "non_finite": bad, "elements": int(g.size), "rows": "every row",
+            "ok": bool(bad == 0 and max_abs <= ABS_TOL and max_rel <= REL_TOL)}
+
+
+def converter_exact(orc, bsf, n: int, rp, ci) -> dict:
+    """The GPU converter's offsets, block columns and row masks against the
+    oracle converter (src/converter.cu:13-44 restated, plus masks), bit for
+    bit; the oracle's wall time on the checker threads beside it."""
+    t0 = time.perf_counter()
+    offs, bcol, mask = orc.convert(n, rp, ci)
+    dt = time.perf_counter() - t0
+    hb = bsf.to_host()
+    same = (np.array_equal(hb.window_offsets, offs) and np.array_equal(hb.block_col_indices, bcol)
+            and np.array_equal(hb.tile_masks, mask))
+    return {"tile_lists_bit_exact": bool(same), "row_windows": int(len(offs) - 1),
+            "active_tiles": int(len(bcol)), "oracle_converter_s": dt,
+            "compared": "window_offsets, block_col_indices and tile_masks, every entry"}
+
+
+def reference_single_thread(rp, ci, Q, K, V, n: int, d: int, min_s: float = 0.5) -> dict | None:
+    """The reference's cpu_sparse_attention_csr (baselines/cpu_baseline.cpp,
+    compiled in place under oracle/_ref), one thread, over the whole graph and
+    head 0 (the reference is single-head); repeated until `min_s` seconds
+    have passed on small graphs, mean time per call."""
     ref = ROOT / "oracle" / "_ref" / "libref_cpu_baseline.so"
-    kind = "reference"
     if not ref.exists():
         return None
     lib = C.CDLL(str(ref))
     fn = lib.ref_cpu_sparse_attention_csr
     fn.restype = None
     fn.argtypes = [C.c_int32, C.c_int32] + [C.c_void_p] * 6
-    Qf, Kf, Vf = (np.ascontiguousarray(x.reshape(n, d), np.float32) for x in (Q, K, V))
+    Qf, Kf, Vf = (np.ascontiguousarray(x.reshape(n, -1, d)[:, 0, :], np.float32)
+                  for x in (Q, K, V))
+    rp32 = np.ascontiguousarray(rp, np.int32)
+    ci32 = np.ascontiguousarray(ci, np.int32)
     O = np.zeros((n, d), np.float32)
+    calls = 0
     t0 = time.perf_counter()
-    fn(n, d, Qf.ctypes.data, Kf.ctypes.data, Vf.ctypes.data, rp.ctypes.data, ci.ctypes.data,
-       O.ctypes.data)
-    dt = time.perf_counter() - t0
+    while True:
+        fn(n, d, Qf.ctypes.data, Kf.ctypes.data, Vf.ctypes.data, rp32.ctypes.data,
+           ci32.ctypes.data, O.ctypes.data)
+        calls += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            break
     edges = int(rp[n])
-    return {"value": edges / dt, "unit": "edges/s", "cores": 1, "kind": kind,
-            "sample": f"all {n} rows / {edges} edges of the workload, one call, "
-                      f"{dt:.2f} s on {os.cpu_count()} visible host cores (1 used)",
+    per = dt / calls
+    return {"value": edges / per, "unit": "edges/s", "cores": 1, "kind": "reference",
+            "sample": f"all {n} rows / {edges} edges, head 0 (the reference is single-head), "
+                      f"{calls} call(s), {per:.4f} s per call on 1 thread",
             "threads_used": 1, "cores_available": len(os.sched_getaffinity(0)),
             "cpu_model": host_cpu_model()}
 
 
-def cpu_baseline_all_cores(rp, ci, Q, K, V, n: int, H: int, d: int) -> dict | None:
-    """The CPU restatement of cpu_sparse_attention_csr (oracle/f3s_oracle.c,
-    OpenMP over rows) on the host cores this process may use, at most 16 (a
-    one-GPU box's CPU share), over the whole graph and every head."""
-    lib_path = ROOT / "oracle" / "liboracle.so"
-    if not lib_path.exists():
-        return None
-    lib = C.CDLL(str(lib_path))
-    fn = lib.orc_masked_attention
-    fn.restype = None
-    fn.argtypes = ([C.c_int32] * 3 + [C.c_void_p] * 5 + [C.c_float, C.c_int32, C.c_int32,
-                                                         C.c_void_p, C.c_int32])
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    Qf, Kf, Vf = (np.ascontiguousarray(x.reshape(n, H, d), np.float32) for x in (Q, K, V))
-    rp32 = np.ascontiguousarray(rp, np.int32)
-    ci32 = np.ascontiguousarray(ci, np.int32)
-    O = np.zeros((n, H, d), np.float32)
-    t0 = time.perf_counter()
-    fn(n, d, H, Qf.ctypes.data, Kf.ctypes.data, Vf.ctypes.data, rp32.ctypes.data,
-       ci32.ctypes.data, 1.0, 0, n, O.ctypes.data, threads)
-    dt = time.perf_counter() - t0
-    edges = int(rp[n])
-    return {"value": edges / dt, "unit": "edges/s", "cores": threads, "kind": "port",
-            "sample": f"all {n} rows / {edges} edges x {H} head(s), one call, {dt:.2f} s on "
-                      f"{threads} threads (OpenMP) of {len(os.sched_getaffinity(0))} available cores",
-            "threads_used": threads, "cores_available": len(os.sched_getaffinity(0)),
-            "cpu_model": host_cpu_model()}
+def config_legs(f3s, orc, cfgnum: int, stream, reps_masked: int = 20,
+                reps_dense: int = 5) -> dict:
+    """One configuration end to end on the GPU, then checked on the host:
+    converter (GPU time of its two phases; output bit-exact against the
+    oracle converter), the planned masked and tile-dense passes and the
+    drop-in launch f3s_attention_fwd in the reference's descending order in
+    both semantics (mean of HIP events per pass on the launch stream), each
+    output compared on every row with the fp32 oracle after all GPU timing;
+    the reference's single-thread CPU baseline (head 0) and the CPU
+    restatement on all checker threads (every head) beside them."""
+    c = f3s.CONFIGS[cfgnum]
+    t0 = time.time()
+    rp, ci = c.graph()
+    n, H, d = c.n, c.H, c.d
+    nnz = int(len(ci))
+    Q, K, V = (c.features(t) for t in range(3))
+    print(f"[bench] leg cfg{cfgnum} {c.name}: n={n} nnz={nnz} H={H} inputs "
+          f"{time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    csr = f3s.DeviceCSR(rp, ci, stream)
+    bsf = f3s.convert_device(csr, masks=True, stream=stream)
+    f3s.synchronize()
+    conv_ms = convert_phases_ms(csr, bsf, stream)
+    order = f3s.window_order_device(bsf, stream)
+    plan = f3s.Plan(bsf, order, H=H, stream=stream)
+    plan.compile(stream)
+    ps = plan.stats()
+    occ_sum, mask_bits = f3s.bsf_stats(bsf, True, stream)
+    dQ, dK, dV = (f3s.DeviceArray.from_numpy(x.view(np.uint16), stream) for x in (Q, K, V))
+    dO = f3s.DeviceArray((n, H, d), np.float32)
+    kv_rows = {True: kv_rows_needed(n, ci, None, True),
+               False: kv_rows_needed(n, ci, bsf.block_col.numpy(), False)}
+    runs = [
+        ("masked_planned", lambda: plan.forward(dQ, dK, dV, dO, masked=True, stream=stream),
+         True, "plan", reps_masked),
+        ("tile_dense_planned", lambda: plan.forward(dQ, dK, dV, dO, masked=False, stream=stream),
+         False, "plan", reps_dense),
+        ("dropin_descending_masked",
+         lambda: f3s.attention_fwd(dQ, dK, dV, dO, bsf, order, masked=True, H=H, d=d,
+                                   stream=stream), True, "unplanned", reps_masked),
+        ("dropin_descending_tile_dense",
+         lambda: f3s.attention_fwd(dQ, dK, dV, dO, bsf, order, masked=False, H=H, d=d,
+                                   stream=stream), False, "unplanned", reps_dense),
+    ]
+    legs, outs = {}, {}
+    for name, fn, sem, lnch, reps in runs:
+        dO.fill_bytes(0xFF, stream)   # NaN: a row the pass does not write cannot match
+        t = time_passes(f3s, fn, stream, reps)
+        mean = float(t.mean())
+        b = compulsory_bytes(n, H, bsf.W, bsf.T, kv_rows[sem], sem, lnch, ps)
+        chunks = (ps["num_chunks"] if (sem and lnch == "plan") else
+                  (occ_sum + 31) // 32 if sem else (bsf.T + 1) // 2)
+        issued = chunks * H * 8 * (2 * 16 * 16 * 32)
+        tile_model = bsf.T * 4 * 16 * 16 * d * H
+        legs[name] = {"semantics": "masked" if sem else "tile_dense", "launch": lnch,
+                      "kernel_us": mean * 1e3, "kernel_us_min": float(t.min()) * 1e3,
+                      "passes": reps, "edges_per_s": nnz / (mean * 1e-3),
+                      "compulsory_bytes": b,
+                      "roofline_frac": b / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                      "mfma_issued_frac": issued / (mean * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
+                      "mfma_tile_model_frac": tile_model / (mean * 1e-3)
+                      / (MFMA_F16_PEAK_TFLOPS * 1e12)}
+        outs[name] = dO.numpy()
+    del dQ, dK, dV, dO, plan, order, csr
+    # ---- host side, after every GPU timing: checker and CPU baselines
+    print(f"[bench] leg cfg{cfgnum}: checking every row on the host ...", file=sys.stderr,
+          flush=True)
+    res = {"workload": f"cfg{c.cfg}: {c.name}", "nodes": n, "edges": nnz, "heads": H,
+           "head_dim": d, "row_windows": bsf.W, "active_tiles": bsf.T,
+           "attended_tile_columns": occ_sum, "mask_bits": mask_bits,
+           "converter_us": conv_ms * 1e3}
+    res["converter_check"] = converter_exact(orc, bsf, n, rp, ci)
+    offs = bsf.window_offsets.numpy()
+    bcol = bsf.block_col.numpy()
+    del bsf
+    Qf, Kf, Vf = (x.astype(np.float32) for x in (Q, K, V))
+    thr = check_threads()
+    t1 = time.perf_counter()
+    want_m = orc.masked_attention(n, d, H, Qf, Kf, Vf, rp, ci, threads=thr)
+    masked_s = time.perf_counter() - t1
+    t1 = time.perf_counter()
+    want_d = orc.tile_dense_attention(n, d, H, Qf, Kf, Vf, offs, bcol, threads=thr, fast=True)
+    dense_s = time.perf_counter() - t1
+    for name, leg in legs.items():
+        leg["check"] = compare_rows(outs.pop(name),
+                                    want_m if leg["semantics"] == "masked" else want_d)
+    del want_m, want_d
+    res["legs"] = legs
+    res["verified"] = bool(res["converter_check"]["tile_lists_bit_exact"]
+                           and all(l["check"]["ok"] for l in legs.values()))
+    res["oracle_s"] = {"masked_all_rows": masked_s, "tile_dense_all_rows": dense_s,
+                       "threads": thr}
+    res["cpu_baseline"] = reference_single_thread(rp, ci, Qf, Kf, Vf, n, d)
+    res["cpu_baseline_all_cores"] = {
+        "value": nnz / masked_s, "unit": "edges/s", "cores": thr, "kind": "port",
+        "sample": f"all {n} rows / {nnz} edges x {H} head(s): the masked oracle run that "
+                  f"checked the legs, {masked_s:.2f} s on {thr} threads (OpenMP)",
+        "cpu_model": host_cpu_model()}
+    return res
 
 
 def main() -> int:
@@ -378,7 +519,13 @@ def main() -> int:
     ap.add_argument("--no-reference-launches", action="store_true",
                     help="skip timing the reference's semantics and launch shape, and the "
                          "flow from host memory, after the timed region")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the CPU leg: CPU baselines, the checker of every timed output, "
+                         "and the other configurations")
+    ap.add_argument("--configs", default="2,3,5",
+                    help="comma-separated configurations measured and checked after the "
+                         "headline, each in both semantics, planned and through the drop-in "
+                         "launch (empty: none)")
     ap.add_argument("--gather-probe", action="store_true",
                     help="only measure the random-gather ceiling (f3s_probe_gather) over "
                          "tables of several sizes and exit")
@@ -547,6 +694,8 @@ def main() -> int:
     kern_ms = np.array([a.elapsed_ms(b) for a, b in evs])
     ms_per_step = wall * 1e3 / args.steps
     kavg = float(kern_ms.mean())
+    # the last timed pass's output, checked on every row in the CPU leg
+    head_out = dO.numpy(stream)
 
     launch = "unplanned" if args.unplanned else "plan"
     kv_rows = {True: kv_rows_needed(n, ci, None, True)}
@@ -653,6 +802,7 @@ def main() -> int:
                   "tile-dense: 16 per tile) per second by the ceiling of its semantics")
     res["gather_ceiling"] = gc
 
+    legs, leg_outs = {}, {}
     if not args.no_reference_launches:
         # The reference's own semantics (tile-dense, src/fused3s_v2.cu:145-228)
         # and launch shape (every window whole, descending order, one launch:
@@ -664,16 +814,18 @@ def main() -> int:
         occ_masked = occ_sum if masked else f3s.bsf_stats(bsf, True, stream)[0]
         ref_plan = plan if plan is not None else make_plan()
         rps = ref_plan.stats()
-        legs = {}
         reps_m = max(3, min(20, args.steps))
         reps_d = max(3, min(5, args.steps))
 
         def leg(name, fn, sem_masked, lnch, reps):
+            dO.fill_bytes(0xFF, stream)   # NaN: a row the pass does not write cannot match
             t = time_passes(f3s, fn, stream, reps)
             mean = float(t.mean())
+            leg_outs[name] = dO.numpy(stream)
             b = compulsory_bytes(n, H, bsf.W, bsf.T, kv_rows[sem_masked], sem_masked, lnch, rps)
             rows = 2 * H * (occ_masked if sem_masked else bsf.T * 16)
-            legs[name] = {"kernel_us": mean * 1e3, "edges_per_s": nnz / (mean * 1e-3),
+            legs[name] = {"semantics": "masked" if sem_masked else "tile_dense",
+                          "kernel_us": mean * 1e3, "edges_per_s": nnz / (mean * 1e-3),
                           "passes": reps, "compulsory_bytes": b,
                           "roofline_frac": b / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS,
                           "gathered_rows_per_s": rows / (mean * 1e-3),
@@ -698,15 +850,57 @@ def main() -> int:
         res["host_handover"] = host_handover(f3s, rp, ci, Q, K, V, n, H, d, masked)
 
     if not args.no_cpu_baseline:
+        # The CPU leg, after every GPU timing: the reference's CPU baseline,
+        # its restatement on all checker threads, and the checker -- the GPU
+        # converter's output bit for bit and every timed pass's output on
+        # every row, against the oracle (tests/test_fused_3s_v2.cu:137-155
+        # checks the launch it timed the same way).
+        orc = oracle_module()
+        thr = check_threads()
         print("[bench] timing the reference CPU baseline ...", file=sys.stderr, flush=True)
-        res["cpu_baseline"] = cpu_baseline(rp, ci, Q.astype(np.float32), K.astype(np.float32),
-                                           V.astype(np.float32), n, d) if H == 1 else None
-        print("[bench] timing the CPU restatement on all available cores ...", file=sys.stderr,
+        Qf, Kf, Vf = (x.astype(np.float32) for x in (Q, K, V))
+        res["cpu_baseline"] = reference_single_thread(rp, ci, Qf, Kf, Vf, n, d)
+        print("[bench] checking the converter and every timed output ...", file=sys.stderr,
               flush=True)
-        res["cpu_baseline_all_cores"] = cpu_baseline_all_cores(rp, ci, Q, K, V, n, H, d)
-        print("[bench] timing the tile-dense oracle on a sample ...", file=sys.stderr, flush=True)
-        res["tile_dense_oracle"] = tile_dense_oracle(Q, K, V, bsf.window_offsets.numpy(),
-                                                     bsf.block_col.numpy(), n, H, d)
+        ver = {"converter": converter_exact(orc, bsf, n, rp, ci)}
+        t1 = time.perf_counter()
+        want_m = orc.masked_attention(n, d, H, Qf, Kf, Vf, rp, ci, threads=thr)
+        masked_s = time.perf_counter() - t1
+        res["cpu_baseline_all_cores"] = {
+            "value": nnz / masked_s, "unit": "edges/s", "cores": thr, "kind": "port",
+            "sample": f"all {n} rows / {nnz} edges x {H} head(s): the masked oracle run that "
+                      f"checks the timed passes, {masked_s:.2f} s on {thr} threads (OpenMP) of "
+                      f"{len(os.sched_getaffinity(0))} available cores",
+            "threads_used": thr, "cores_available": len(os.sched_getaffinity(0)),
+            "cpu_model": host_cpu_model()}
+        want_d = None
+        if not masked or any(l["semantics"] == "tile_dense" for l in legs.values()):
+            t1 = time.perf_counter()
+            want_d = orc.tile_dense_attention(n, d, H, Qf, Kf, Vf, bsf.window_offsets.numpy(),
+                                              bsf.block_col.numpy(), threads=thr, fast=True)
+            dense_s = time.perf_counter() - t1
+            res["tile_dense_oracle"] = {
+                "tiles_per_s": bsf.T * H / dense_s, "threads": thr, "cpu_model": host_cpu_model(),
+                "sample": f"every row: {bsf.T} tiles x {H} head(s), {dense_s:.2f} s on {thr} "
+                          "threads (each window's 16 rows in AVX2 lanes, bit-identical to the "
+                          "scalar restatement)"}
+        ver["headline"] = compare_rows(head_out, want_m if masked else want_d)
+        for name, out in leg_outs.items():
+            legs[name]["check"] = compare_rows(out, want_m if legs[name]["semantics"] == "masked"
+                                               else want_d)
+        res["verification"] = ver
+        del head_out, leg_outs, want_m, want_d, Qf, Kf, Vf
+        cfgs = [int(x) for x in args.configs.split(",") if x.strip()] if args.configs else []
+        if cfgs:
+            res["configs"] = {}
+        for k in cfgs:
+            if k == c.cfg and not args.heads:
+                continue
+            res["configs"][f"cfg{k}"] = config_legs(f3s, orc, k, stream)
+        res["verified"] = bool(
+            ver["converter"]["tile_lists_bit_exact"] and ver["headline"]["ok"]
+            and all(l["check"]["ok"] for l in legs.values())
+            and all(v["verified"] for v in res.get("configs", {}).values()))
     print(json.dumps(res), flush=True)
     return 0
 

@@ -361,6 +361,166 @@ void orc_tile_dense_attention(int32_t n, int32_t d, int32_t H,
     }
 }
 
+/* The same TILE_DENSE truth, one window at a time with its 16 rows as SIMD
+ * lanes (a window's rows attend the same columns).  Every lane performs the
+ * scalar restatement's operations in the scalar restatement's order -- each
+ * dot product over f = 0..63 (multiply, then add: no contraction), the max
+ * from -1e9 in column order (MAXPS(a, b) is a > b ? a : b, the scalar
+ * form's comparison), expf per element, the sum in column order, the
+ * division, and per feature the weighted sum in column order -- so the
+ * result is bit-identical to orc_tile_dense_attention (tests/test_oracle.py
+ * checks it); only the arithmetic runs in AVX2 vectors.  Hosts without AVX2,
+ * and head sizes other than 64, run the scalar form. */
+#pragma GCC push_options
+#pragma GCC target("avx2")
+#include <immintrin.h>
+
+#define TD_D 64       /* the fast form's head size (the only one the path supports) */
+#define TD_COLS 4     /* columns whose dot products run interleaved */
+#define TD_BLOCK 64   /* columns per block of the weighted V sum */
+
+static const float td_zero_row[TD_D] __attribute__((aligned(32)));
+
+static void td_window(int32_t n, int32_t H, const float* Q, const float* K, const float* V,
+                      int32_t b0, int32_t b1, const int32_t* block_col, float scale, int32_t lo,
+                      int32_t hi, int32_t h, float* O, __m256* S, int32_t* gcs, __m256* qT,
+                      __m256* acc)
+{
+    const int32_t row0 = lo & ~15;
+    const int64_t len = (int64_t)(b1 - b0) * 16;
+    /* qT[2f], qT[2f+1] = {Q[row0 + r][h][f] : r = 0..15} (rows outside [lo, hi) zero) */
+    for (int32_t f = 0; f < TD_D; ++f) {
+        float t[16];
+        for (int r = 0; r < 16; ++r) {
+            const int32_t row = row0 + r;
+            t[r] = (row >= lo && row < hi) ? Q[((int64_t)row * H + h) * TD_D + f] : 0.0f;
+        }
+        qT[2 * f] = _mm256_loadu_ps(t);
+        qT[2 * f + 1] = _mm256_loadu_ps(t + 8);
+    }
+    for (int64_t x = 0; x < len; ++x) gcs[x] = block_col[b0 + x / 16] * 16 + (int32_t)(x % 16);
+    /* logits, TD_COLS columns at a time (independent dot products) */
+    const __m256 vscale = _mm256_set1_ps(scale), vlow = _mm256_set1_ps(-1e9f);
+    for (int64_t x = 0; x < len; x += TD_COLS) {
+        const float* kp[TD_COLS];
+        __m256 a0[TD_COLS], a1[TD_COLS];
+        for (int j = 0; j < TD_COLS; ++j) {
+            const int32_t gc = gcs[x + j];
+            kp[j] = gc < n ? K + ((int64_t)gc * H + h) * TD_D : td_zero_row;
+            a0[j] = _mm256_setzero_ps();
+            a1[j] = _mm256_setzero_ps();
+        }
+        for (int32_t f = 0; f < TD_D; ++f) {
+            const __m256 q0 = qT[2 * f], q1 = qT[2 * f + 1];
+            for (int j = 0; j < TD_COLS; ++j) {
+                const __m256 kb = _mm256_broadcast_ss(kp[j] + f);
+                a0[j] = _mm256_add_ps(a0[j], _mm256_mul_ps(q0, kb));
+                a1[j] = _mm256_add_ps(a1[j], _mm256_mul_ps(q1, kb));
+            }
+        }
+        for (int j = 0; j < TD_COLS; ++j) {
+            const int valid = gcs[x + j] < n;
+            S[2 * (x + j)] = valid ? _mm256_mul_ps(a0[j], vscale) : vlow;
+            S[2 * (x + j) + 1] = valid ? _mm256_mul_ps(a1[j], vscale) : vlow;
+        }
+    }
+    __m256 mx0 = vlow, mx1 = vlow;
+    for (int64_t x = 0; x < len; ++x) {
+        mx0 = _mm256_max_ps(S[2 * x], mx0);
+        mx1 = _mm256_max_ps(S[2 * x + 1], mx1);
+    }
+    float mx[16];
+    _mm256_storeu_ps(mx, mx0);
+    _mm256_storeu_ps(mx + 8, mx1);
+    __m256 sum0 = _mm256_setzero_ps(), sum1 = sum0;
+    for (int64_t x = 0; x < len; ++x) {
+        float* e = (float*)&S[2 * x];
+        for (int r = 0; r < 16; ++r) e[r] = expf(e[r] - mx[r]);
+        sum0 = _mm256_add_ps(sum0, S[2 * x]);
+        sum1 = _mm256_add_ps(sum1, S[2 * x + 1]);
+    }
+    for (int64_t x = 0; x < len; ++x) {
+        S[2 * x] = _mm256_div_ps(S[2 * x], sum0);
+        S[2 * x + 1] = _mm256_div_ps(S[2 * x + 1], sum1);
+    }
+    /* O[row][f] = sum over columns < n, in column order, of P * V[col][f];
+     * acc holds the 16 rows' 64 running sums (8 vectors a row), blocks of
+     * TD_BLOCK columns */
+    for (int32_t i = 0; i < 16 * 8; ++i) acc[i] = _mm256_setzero_ps();
+    for (int64_t x0 = 0; x0 < len; x0 += TD_BLOCK) {
+        const int64_t x1 = x0 + TD_BLOCK < len ? x0 + TD_BLOCK : len;
+        for (int32_t r = lo - row0; r < hi - row0; ++r) {
+            __m256 a[8];
+            for (int k = 0; k < 8; ++k) a[k] = acc[8 * r + k];
+            for (int64_t x = x0; x < x1; ++x) {
+                if (gcs[x] >= n) continue;
+                const float* vrow = V + ((int64_t)gcs[x] * H + h) * TD_D;
+                const __m256 p = _mm256_broadcast_ss((const float*)&S[2 * x] + r);
+                for (int k = 0; k < 8; ++k)
+                    a[k] = _mm256_add_ps(a[k], _mm256_mul_ps(p, _mm256_loadu_ps(vrow + 8 * k)));
+            }
+            for (int k = 0; k < 8; ++k) acc[8 * r + k] = a[k];
+        }
+    }
+    for (int32_t row = lo; row < hi; ++row)
+        for (int k = 0; k < 8; ++k)
+            _mm256_storeu_ps(O + ((int64_t)row * H + h) * TD_D + 8 * k, acc[8 * (row - row0) + k]);
+}
+
+static void td_all(int32_t n, int32_t H, const float* Q, const float* K, const float* V,
+                   const int32_t* window_offsets, const int32_t* block_col, float scale,
+                   int32_t r0, int32_t r1, float* O, int32_t threads)
+{
+    const int32_t w0 = r0 / 16, w1 = (r1 - 1) / 16 + 1;
+#pragma omp parallel num_threads(threads)
+    {
+        int64_t cap = 0;
+        __m256* S = NULL;
+        int32_t* gcs = NULL;
+        __m256* qT = (__m256*)aligned_alloc(32, sizeof(__m256) * 2 * TD_D);
+        __m256* acc = (__m256*)aligned_alloc(32, sizeof(__m256) * 16 * 8);
+#pragma omp for schedule(dynamic, 1)
+        for (int32_t w = w0; w < w1; ++w) {
+            const int32_t b0 = window_offsets[w], b1 = window_offsets[w + 1];
+            const int64_t len = (int64_t)(b1 - b0) * 16;
+            if (len == 0) continue;               /* empty window: O untouched (:42) */
+            if (len > cap) {
+                free(S); free(gcs);
+                cap = len;
+                S = (__m256*)aligned_alloc(32, sizeof(__m256) * 2 * (size_t)cap);
+                gcs = (int32_t*)malloc(sizeof(int32_t) * (size_t)cap);
+            }
+            const int32_t lo = w * 16 > r0 ? w * 16 : r0;
+            const int32_t hi = w * 16 + 16 < r1 ? w * 16 + 16 : r1;
+            for (int32_t h = 0; h < H; ++h)
+                td_window(n, H, Q, K, V, b0, b1, block_col, scale, lo, hi, h, O, S, gcs, qT, acc);
+        }
+        free(S);
+        free(gcs);
+        free(qT);
+        free(acc);
+    }
+}
+#pragma GCC pop_options
+
+void orc_tile_dense_attention_fast(int32_t n, int32_t d, int32_t H,
+                                   const float* Q, const float* K, const float* V,
+                                   const int32_t* window_offsets, const int32_t* block_col,
+                                   float scale, int32_t r0, int32_t r1, float* O,
+                                   int32_t threads)
+{
+    if (d != TD_D || !__builtin_cpu_supports("avx2")) {
+        orc_tile_dense_attention(n, d, H, Q, K, V, window_offsets, block_col, scale, r0, r1, O,
+                                 threads);
+        return;
+    }
+    if (threads < 1) threads = 1;
+    if (r1 > n) r1 = n;
+    if (r0 < 0) r0 = 0;
+    if (r0 >= r1) return;
+    td_all(n, H, Q, K, V, window_offsets, block_col, scale, r0, r1, O, threads);
+}
+
 /* ------------------------------------------------------------- occupancy */
 
 void orc_bsf_occupancy(int32_t n, int64_t T, const int32_t* block_col,

@@ -74,6 +74,16 @@ void orc_tile_dense_attention(int32_t n, int32_t d, int32_t H,
                               float scale, int32_t r0, int32_t r1, float* O,
                               int32_t threads);
 
+/* The same TILE_DENSE truth with each window's 16 rows in SIMD lanes: the
+ * scalar restatement's operations in its order, lane by lane, hence
+ * bit-identical to orc_tile_dense_attention (checked by tests/test_oracle.py);
+ * fast enough to check every row of the large configurations. */
+void orc_tile_dense_attention_fast(int32_t n, int32_t d, int32_t H,
+                                   const float* Q, const float* K, const float* V,
+                                   const int32_t* window_offsets, const int32_t* block_col,
+                                   float scale, int32_t r0, int32_t r1, float* O,
+                                   int32_t threads);
+
 /* Occupancy figures behind the algorithmic byte model: occ_sum = sum over
  * tiles of occ(t), where occ(t) = popcount of the OR of the tile's 16 row
  * masks (masked) or the number of the tile's columns < n (tile-dense);

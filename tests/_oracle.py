@@ -32,6 +32,8 @@ _API = {
                                     _vp, _i32]),
     "orc_tile_dense_attention": (None, [_i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _f32, _i32,
                                         _i32, _vp, _i32]),
+    "orc_tile_dense_attention_fast": (None, [_i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _f32,
+                                             _i32, _i32, _vp, _i32]),
     "orc_bsf_occupancy": (None, [_i32, _i64, _vp, _vp, C.c_int, C.POINTER(_i64), C.POINTER(_i64)]),
 }
 
@@ -128,14 +130,17 @@ def masked_attention(n, d, H, Q, K, V, row_ptr, col_idx, scale=1.0, r0=0, r1=Non
     return O
 
 
-def tile_dense_attention(n, d, H, Q, K, V, offs, bcol, scale=1.0, r0=0, r1=None, threads=8):
+def tile_dense_attention(n, d, H, Q, K, V, offs, bcol, scale=1.0, r0=0, r1=None, threads=8,
+                         fast=False):
+    """TILE_DENSE truth; fast=True runs orc_tile_dense_attention_fast (the
+    same bits, each window's rows in SIMD lanes)."""
     r1 = n if r1 is None else r1
     Q, K, V = (np.ascontiguousarray(x, np.float32) for x in (Q, K, V))
     offs = np.ascontiguousarray(offs, np.int32)
     bcol = np.ascontiguousarray(bcol if len(bcol) else np.zeros(1, np.int32), np.int32)
     O = np.zeros((n, H, d), np.float32)
-    lib().orc_tile_dense_attention(n, d, H, _p(Q), _p(K), _p(V), _p(offs), _p(bcol), scale,
-                                   r0, r1, _p(O), threads)
+    fn = lib().orc_tile_dense_attention_fast if fast else lib().orc_tile_dense_attention
+    fn(n, d, H, _p(Q), _p(K), _p(V), _p(offs), _p(bcol), scale, r0, r1, _p(O), threads)
     return O
 
 

@@ -24,6 +24,10 @@ How each oracle function is pinned (none is left "parity unpinned"):
   orc_tile_dense_attention          equals the reference's cpu_sparse_attention_csr
                                     run on the tile-expanded CSR (bit-identical);
                                     closed forms
+  orc_tile_dense_attention_fast     the same two checks, and bit-identical to
+                                    orc_tile_dense_attention on random graphs
+                                    (heads, scale, row ranges, empty graphs) and
+                                    on config 4's windows, its hub included
   orc_bsf_occupancy                 numpy popcounts
 """
 from __future__ import annotations
@@ -271,6 +275,49 @@ def test_tile_dense_oracle_equals_reference_on_expanded_csr():
         ref = orc.ref_masked_attention(n, d, Q, K, V, erp.astype(np.int32), eci)
         got = orc.tile_dense_attention(n, d, 1, Q, K, V, offs, bcol)[:, 0, :]
         assert np.array_equal(ref.view(np.uint32), got.view(np.uint32))
+        fast = orc.tile_dense_attention(n, d, 1, Q, K, V, offs, bcol, fast=True)[:, 0, :]
+        assert np.array_equal(ref.view(np.uint32), fast.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,deg,seed,H,scale,r0,r1", [
+    (37, 5, 1, 1, 1.0, 0, None),      # n % 16 != 0: padded columns of the last block column
+    (200, 9, 2, 2, 0.7, 5, 197),      # a logit scale, partial first and last windows
+    (1000, 30, 3, 1, 1.0, 0, None),   # dense windows
+    (777, 4, 4, 3, 1.0, 16, 700),     # three heads
+    (5000, 12, 5, 4, 1.0, 0, None),
+    (300, 0, 6, 1, 1.0, 0, None),     # no edges at all: every window empty, O untouched
+])
+def test_tile_dense_fast_equals_scalar(n, deg, seed, H, scale, r0, r1):
+    """orc_tile_dense_attention_fast (each window's 16 rows in SIMD lanes)
+    gives the scalar restatement's bits on every row it computes and leaves
+    the others untouched."""
+    if deg:
+        rp, ci = random_csr(n, deg, seed, self_loops=bool(seed % 2))
+    else:
+        rp, ci = np.zeros(n + 1, np.int32), np.zeros(0, np.int32)
+    offs, bcol, _ = orc.convert(n, rp, ci)
+    Q, K, V = (f16_inputs((n, H, 64), seed * 10 + s, normal=bool(seed % 2)) for s in range(3))
+    a = orc.tile_dense_attention(n, 64, H, Q, K, V, offs, bcol, scale=scale, r0=r0, r1=r1)
+    b = orc.tile_dense_attention(n, 64, H, Q, K, V, offs, bcol, scale=scale, r0=r0, r1=r1,
+                                 fast=True)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_tile_dense_fast_equals_scalar_on_config4_windows():
+    """The two forms agree bit for bit on config 4's first 300 windows and on
+    its heaviest window (a hub of thousands of tiles), N(0, 1) inputs."""
+    import fused3s_amd as f3s
+    c = f3s.CONFIGS[4]
+    rp, ci = c.graph()
+    n = c.n
+    offs, bcol, _ = orc.convert(n, rp, ci)
+    Q, K, V = (c.features(t).astype(np.float32) for t in range(3))
+    hub = int(np.argmax(np.diff(offs)))
+    assert offs[hub + 1] - offs[hub] > 1000
+    for r0, r1 in ((0, 16 * 300), (16 * hub, min(n, 16 * hub + 16))):
+        a = orc.tile_dense_attention(n, 64, 1, Q, K, V, offs, bcol, r0=r0, r1=r1)
+        b = orc.tile_dense_attention(n, 64, 1, Q, K, V, offs, bcol, r0=r0, r1=r1, fast=True)
+        assert np.array_equal(a[r0:r1].view(np.uint32), b[r0:r1].view(np.uint32))
 
 
 @pytest.mark.parametrize("n,deg,seed,scale", [(50, 4, 1, 1.0), (200, 9, 2, 0.125), (97, 30, 3, 1.0)])
