@@ -15,8 +15,10 @@ struct f3s_item_set {
 
 struct f3s_plan {
     int32_t W = 0, H = 1;
-    int32_t xcd_contiguous = 1;  // items map to XCDs in contiguous ranges (scheduled
-                                 // items, or natural order: neighbours share an L2)
+    int32_t xcd_contiguous = 1;  // natural-order, unscheduled plans: items map to XCDs in
+                                 // contiguous ranges (neighbours share an L2); scheduled
+                                 // plans are dealt round-robin, their i*8+x slot
+                                 // interleave already lining shares up with the XCDs
     int64_t T = 0;
     // Masked passes (compiled lists or tile expansion) run `masked`.  A
     // tile-dense chunk costs two whole tiles, about 15x a masked chunk per

@@ -58,6 +58,9 @@ void dev_free_idle(void* ptr, int device);
 // Waits for every stream of `device`, then returns `ptr` for reuse: for
 // memory whose last users may be on any stream (hipFree's behaviour).
 void dev_free_synced(void* ptr, int device);
+// dev_free_synced for caller-owned memory (f3s_free): blocks of 64 MiB and
+// more go back to the driver (hipFree), smaller ones to the cache.
+void dev_free_to_driver_if_large(void* ptr, int device);
 // Host-pinned staging words of the calling thread (16 x int64), for the small
 // device-to-host reads of counts and status that size outputs.
 int64_t* host_staging();
@@ -79,7 +82,7 @@ struct DeviceBuffer {
 };
 
 // Scratch memory of one call: allocated on the call's stream and returned to
-// the pool in stream order when it goes out of scope, so a call that queues
+// the cache in stream order when it goes out of scope, so a call that queues
 // work on the stream and returns without waiting may still use it on the
 // device.  The stream must outlive the object (it does for call-local use).
 struct StreamBuffer {

@@ -113,6 +113,14 @@ void save_graph_binary(const std::string& path, const GraphData& g, const blockS
         throw std::runtime_error(f3s_host_last_error());
 }
 
+// Distinct (row, column) pairs the masks record.
+static int64_t mask_popcount(const std::vector<uint16_t>& masks)
+{
+    int64_t bits = 0;
+    for (uint16_t m : masks) bits += __builtin_popcount(m);
+    return bits;
+}
+
 GraphData load_graph_binary(const std::string& path, blockSparseFormat* bsf)
 {
     int32_t n = 0, W = 0;
@@ -132,7 +140,10 @@ GraphData load_graph_binary(const std::string& path, blockSparseFormat* bsf)
             bsf->num_row_windows = W;
             bsf->window_offsets.assign(wo, wo + W + 1);
             bsf->block_col_indices.assign(bc, bc + T);
-            if (tm) bsf->tile_masks.assign(tm, tm + 16 * T);
+            if (tm) {
+                bsf->tile_masks.assign(tm, tm + 16 * T);
+                bsf->duplicate_entries = nnz - mask_popcount(bsf->tile_masks);
+            }
         }
     }
     for (void* p : {(void*)rp, (void*)ci, (void*)wo, (void*)bc, (void*)tm}) free(p);
@@ -177,8 +188,14 @@ blockSparseFormat convert_csr_to_block_sparse(int num_nodes, const std::vector<i
               "d2h");
         check(f3s_memcpy_d2h(bsf.tile_masks.data(), mask.p, 32 * (size_t)T, nullptr), "d2h");
     }
+    bsf.duplicate_entries = nnz - mask_popcount(bsf.tile_masks);
     std::cout << "Row Windows: " << bsf.num_row_windows << std::endl;
     std::cout << "Total Active Blocks: " << bsf.block_col_indices.size() << std::endl;
+    if (bsf.duplicate_entries > 0)
+        std::cerr << "convert_csr_to_block_sparse: the CSR repeats " << bsf.duplicate_entries
+                  << " entries; tile lists are unaffected, masked attention counts each edge "
+                     "once (cpu_sparse_attention_csr counts every repeat)"
+                  << std::endl;
     return bsf;
 }
 

@@ -35,12 +35,15 @@ gather_probe_kernel(const uint16_t* __restrict__ K, const uint16_t* __restrict__
     const uint32_t piece = 16u * (lane & 7);
     pu4 acc = {0u, 0u, 0u, 0u};
     for (int64_t s = s0; s < s1; ++s) {
-        const uint32_t my = (uint32_t)idx[s * 32 + (lane & 31)];
+        const int32_t my = idx[s * 32 + (lane & 31)];
         pu4 kk[4], vv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t row = (uint32_t)__shfl((int)my, (lane >> 3) + 8 * i);
-            const uint32_t off = row * row_stride + piece;
+            // 64-bit offset, clamped to table_bytes: a negative row or one
+            // past the table reads zero through the descriptor's range check
+            const int64_t row = __shfl(my, (lane >> 3) + 8 * i);
+            const int64_t o = row * (int64_t)row_stride + piece;
+            const uint32_t off = (o >= 0 && o < (int64_t)table_bytes) ? (uint32_t)o : table_bytes;
             kk[i] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
             vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0);
         }

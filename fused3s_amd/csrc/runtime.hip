@@ -1,6 +1,7 @@
 // runtime.hip -- error reporting, device plumbing, fp32->fp16 cast and the
 // device-wide scan used by the converter and the planner.
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <iterator>
 #include <map>
@@ -58,15 +59,19 @@ f3s_status require_device()
 // recorded on its stream at the free; whoever takes it next waits for that
 // event (on the device, through its own stream), so a block is never reused
 // while its last user's work may still run.  Idle cached bytes are capped per
-// device; on an allocation failure the cache is returned to the driver and
-// the allocation retried.
+// device (1 GiB, or F3S_CACHE_LIMIT_MB read at the first allocation; 0 keeps
+// nothing), so a process that shares the GPU with another allocator (torch's)
+// holds little idle memory; f3s_free hands blocks of 64 MiB and more straight
+// back to the driver, as hipFree would; on an allocation failure the cache is
+// returned to the driver and the allocation retried.
 
 namespace {
 
 constexpr int kMaxDevices = 64;
 constexpr size_t kSmallQuantum = 512;
 constexpr size_t kLargeQuantum = (size_t)2 << 20;
-constexpr size_t kCacheCap = (size_t)16 << 30;   // idle cached bytes kept per device
+constexpr size_t kDefaultCacheCap = (size_t)1 << 30;   // idle cached bytes kept per device
+constexpr size_t kReturnToDriver = (size_t)64 << 20;  // f3s_free: from this size, hipFree
 
 struct CachedBlock {
     void* ptr;
@@ -82,6 +87,21 @@ struct DeviceCache {
 
 std::mutex g_mem_mu;
 DeviceCache g_cache[kMaxDevices];
+
+// The idle-byte cap: F3S_CACHE_LIMIT_MB if set to a number, else 1 GiB.
+size_t cache_cap()
+{
+    static const size_t cap = [] {
+        const char* v = getenv("F3S_CACHE_LIMIT_MB");
+        if (v && *v) {
+            char* end = nullptr;
+            const unsigned long long mb = strtoull(v, &end, 10);
+            if (end && *end == '\0' && mb < ((unsigned long long)1 << 44)) return (size_t)mb << 20;
+        }
+        return kDefaultCacheCap;
+    }();
+    return cap;
+}
 
 size_t size_class(size_t bytes)
 {
@@ -112,7 +132,8 @@ void cache_idle(DeviceCache& c, void* ptr, size_t size, hipEvent_t ev)
     c.idle.emplace(size, CachedBlock{ptr, ev});
     c.idle_bytes += size;
     // over the cap: the largest idle blocks go back to the driver
-    while (c.idle_bytes > kCacheCap && !c.idle.empty()) {
+    const size_t cap = cache_cap();
+    while (c.idle_bytes > cap && !c.idle.empty()) {
         auto it = std::prev(c.idle.end());
         c.idle_bytes -= it->first;
         drop_block(c, it->second.ptr, it->second.last_use);
@@ -134,10 +155,12 @@ f3s_status dev_alloc(void** ptr, size_t bytes, hipStream_t stream)
     }
     std::lock_guard<std::mutex> lock(g_mem_mu);
     DeviceCache& c = g_cache[dev];
-    // a cached block of this size class, or a close larger one (at most a
-    // quarter, plus one quantum, bigger)
+    // a cached block of this size class, or a close larger one: at most a
+    // quarter bigger, plus one 2 MiB quantum for the large classes only (a
+    // small request never takes a large block)
     auto it = c.idle.lower_bound(size);
-    if (it != c.idle.end() && it->first <= size + size / 4 + kLargeQuantum) {
+    const size_t slack = size / 4 + (size >= kLargeQuantum / 2 ? kLargeQuantum : 0);
+    if (it != c.idle.end() && it->first <= size + slack) {
         const size_t got = it->first;
         const CachedBlock b = it->second;
         c.idle.erase(it);
@@ -234,6 +257,30 @@ void dev_free_synced(void* ptr, int device)
                             hipSetDevice(device) == hipSuccess;
     (void)hipDeviceSynchronize();
     dev_free_idle(ptr, device);
+    if (switch_dev) (void)hipSetDevice(cur);
+}
+
+void dev_free_to_driver_if_large(void* ptr, int device)
+{
+    if (!ptr) return;
+    bool large = false;
+    if (device >= 0 && device < kMaxDevices) {
+        std::lock_guard<std::mutex> lock(g_mem_mu);
+        DeviceCache& c = g_cache[device];
+        auto it = c.live.find(ptr);
+        if (it != c.live.end() && it->second >= kReturnToDriver) {
+            c.live.erase(it);
+            large = true;
+        }
+    }
+    if (!large) {
+        dev_free_synced(ptr, device);
+        return;
+    }
+    int cur = -1;
+    const bool switch_dev = hipGetDevice(&cur) == hipSuccess && cur != device &&
+                            hipSetDevice(device) == hipSuccess;
+    (void)hipFree(ptr);   // waits for the device, as the caller's hipFree would
     if (switch_dev) (void)hipSetDevice(cur);
 }
 
@@ -475,7 +522,7 @@ f3s_status f3s_malloc(void** ptr, uint64_t bytes)
     F3S_REQUIRE(ptr != nullptr, "f3s_malloc: ptr is NULL");
     *ptr = nullptr;
     F3S_TRY(require_device());
-    // from the device's pool, then usable on every stream (as hipMalloc's memory)
+    // from the device's cache, then usable on every stream (as hipMalloc's memory)
     F3S_TRY(dev_alloc(ptr, bytes, nullptr));
     const hipError_t e = hipStreamSynchronize(nullptr);
     if (e != hipSuccess) {
@@ -499,8 +546,9 @@ f3s_status f3s_free(void* ptr)
         (void)hipGetLastError();
         F3S_HIP(hipGetDevice(&dev));
     }
-    // as hipFree: waits for the device, so no stream still uses the memory
-    dev_free_synced(ptr, dev);
+    // as hipFree: waits for the device, so no stream still uses the memory;
+    // large blocks go back to the driver, smaller ones to the cache
+    dev_free_to_driver_if_large(ptr, dev);
     return F3S_OK;
 }
 

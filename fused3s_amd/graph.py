@@ -6,6 +6,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import sys
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -25,11 +26,22 @@ class GraphData:
 
 @dataclass
 class BlockSparseFormat:
-    """include/utils.cuh:42-46 plus the intra-tile row masks."""
+    """include/utils.cuh:42-46 plus the intra-tile row masks and the number of
+    CSR entries that repeat an earlier (row, column) pair.  With repeats the
+    tile lists are those of the deduplicated CSR (as the reference converter
+    gives), and the masks -- so the masked pass -- count each edge once, where
+    cpu_sparse_attention_csr (baselines/cpu_baseline.cpp:38-50) counts every
+    repeat."""
     num_row_windows: int
     window_offsets: np.ndarray        # int32[W+1]
     block_col_indices: np.ndarray     # int32[T]
     tile_masks: np.ndarray = field(default_factory=lambda: np.zeros((0, 16), np.uint16))  # uint16[T,16]
+    duplicate_entries: int = 0
+
+
+def _mask_bits(masks: np.ndarray) -> int:
+    """Distinct (row, column) pairs the row masks record."""
+    return int(np.unpackbits(np.ascontiguousarray(masks, np.uint16).view(np.uint8)).sum())
 
 
 def _take_i32(ptr, count: int) -> np.ndarray:
@@ -100,8 +112,9 @@ def load_graph(path: str) -> tuple[GraphData, BlockSparseFormat | None]:
                 masks = np.ctypeslib.as_array(tm, shape=(T.value * 16,)).copy().reshape(-1, 16)
         finally:
             lib.f3s_host_free(C.cast(tm, C.c_void_p))
+    dup = int(nnz.value) - _mask_bits(masks) if tm else 0
     return g, BlockSparseFormat(int(W.value), _take_i32(wo, W.value + 1),
-                                _take_i32(bc, T.value), masks)
+                                _take_i32(bc, T.value), masks, dup)
 
 
 class DeviceCSR:
@@ -157,9 +170,14 @@ def convert_csr_to_block_sparse(num_nodes: int, row_ptr, col_ind, verbose: bool 
     if len(row_ptr) != num_nodes + 1:
         raise ValueError("convert_csr_to_block_sparse: row_ptr must hold n+1 entries")
     bsf = convert_device(DeviceCSR(row_ptr, col_ind)).to_host()
+    bsf.duplicate_entries = len(col_ind) - _mask_bits(bsf.tile_masks)
     if verbose:
         print(f"Row Windows: {bsf.num_row_windows}")
         print(f"Total Active Blocks: {len(bsf.block_col_indices)}")
+    if bsf.duplicate_entries > 0:
+        print(f"convert_csr_to_block_sparse: the CSR repeats {bsf.duplicate_entries} entries; "
+              "tile lists are unaffected, masked attention counts each edge once "
+              "(cpu_sparse_attention_csr counts every repeat)", file=sys.stderr)
     return bsf
 
 

@@ -6,10 +6,12 @@
 //   * load_csr_graph reads col_idx.txt (the exporter's name) and throws
 //     std::runtime_error on a missing or malformed file instead of returning
 //     an all-zero graph (utils.cuh:36 opens col_ind.txt and never checks);
-//   * blockSparseFormat carries the new intra-tile row masks;
+//   * blockSparseFormat carries the new intra-tile row masks and the count of
+//     repeated CSR entries;
 //   * convert_csr_to_block_sparse runs on the GPU through libf3s_hip.so
 //     (bit-exact with the reference's host converter) and throws if no GPU
-//     is usable; it prints the same two lines as the reference (:42-43);
+//     is usable; it prints the same two lines as the reference (:42-43), and
+//     a notice on stderr when the CSR repeats entries;
 //   * F3S_CHECK replaces CUDA_CHECK (utils.cuh:9-17) for f3s_status codes.
 #pragma once
 
@@ -44,12 +46,19 @@ struct GraphData {
 GraphData load_csr_graph(const std::string& dataset_dir);
 
 // include/utils.cuh:42-46, plus tile_masks (16 uint16 per active tile: bit c
-// of entry r <=> edge (16w + r, 16*block_col + c)).
+// of entry r <=> edge (16w + r, 16*block_col + c)) and duplicate_entries: CSR
+// entries that repeat an earlier (row, column) pair (nnz minus the masks'
+// popcount).  A CSR with repeats (a multigraph) gives the tile lists of its
+// deduplicated form, as the reference converter does; its masks, and so the
+// masked (edge-exact) pass, count each edge once, whereas the reference's
+// cpu_sparse_attention_csr (baselines/cpu_baseline.cpp:38-50) counts a
+// repeated entry once per repeat.
 struct blockSparseFormat {
     int num_row_windows = 0;
     std::vector<int> window_offsets;
     std::vector<int> block_col_indices;
     std::vector<uint16_t> tile_masks;
+    int64_t duplicate_entries = 0;
 };
 
 // src/converter.cu:13-44

@@ -21,8 +21,7 @@
  *
  * Thread safety: calls on different streams may run concurrently; the
  * library's only mutable global state is the per-thread last error and the
- * per-device memory pools (set up once under a lock; the pool API is
- * thread-safe).
+ * per-device cache of freed device memory (below; one mutex guards it).
  * A plan owns the partial-result buffers of its split windows, so one plan
  * must not serve two overlapping calls.
  */
@@ -67,16 +66,22 @@ f3s_status f3s_init(void);
 f3s_status f3s_device_count(int32_t* count);
 f3s_status f3s_set_device(int32_t device);
 f3s_status f3s_device_name(char* buf, int32_t buflen);
-/* Device memory comes from a stream-ordered pool per device that keeps freed
- * memory for reuse, so repeated allocations (of conversion outputs, plans,
- * scratch) skip the driver's allocation and page mapping.  f3s_malloc'd
- * memory is usable on every stream on return; f3s_free waits for the device
- * first, as hipFree does. */
+/* Device memory comes from a caching allocator over hipMalloc: blocks the
+ * library frees (scratch of a call, in stream order; a destroyed plan's
+ * buffers) are kept per device and size class for reuse, so repeated
+ * conversions, plans and calls skip the driver's allocation and page
+ * mapping.  Idle cached memory is capped per device at 1 GiB, or at the
+ * F3S_CACHE_LIMIT_MB environment variable's value read at the first
+ * allocation (0 keeps nothing); on an allocation failure the cache goes back
+ * to the driver and the allocation is retried.  f3s_malloc'd memory is usable
+ * on every stream on return; f3s_free waits for the device first, as hipFree
+ * does, and returns blocks of 64 MiB and more to the driver at once (smaller
+ * ones to the cache). */
 f3s_status f3s_malloc(void** ptr, uint64_t bytes);
 f3s_status f3s_free(void* ptr);
-/* Returns the memory the pools keep for reuse to the driver (waits for every
- * device first).  No reference counterpart; for processes that share the GPU
- * with another allocator, e.g. torch's. */
+/* Returns every idle cached block to the driver (waits for every device
+ * first).  No reference counterpart; for processes that share the GPU with
+ * another allocator, e.g. torch's. */
 f3s_status f3s_release_cached_memory(void);
 f3s_status f3s_memcpy_h2d(void* dst, const void* src, uint64_t bytes, void* stream);
 f3s_status f3s_memcpy_d2h(void* dst, const void* src, uint64_t bytes, void* stream);
@@ -102,8 +107,15 @@ f3s_status f3s_cast_f32_to_f16(const float* d_in, uint16_t* d_out, int64_t count
  * calls: sizes first (d_block_col = NULL), then the lists.  Output is
  * bit-exact with the reference converter.  F3S_EDATA if row_ptr is not
  * monotone from 0 to nnz or a column is outside [0, n) (the offsets written
- * are then meaningless).  Each call makes one host round trip (to read T and
- * the error bits); scratch comes from the library's pool. */
+ * are then meaningless).  A CSR may repeat an entry (a multigraph): the
+ * reference converter accepts that, and so does this one -- the tile lists
+ * are those of the deduplicated CSR and the masks record each (row, column)
+ * pair once, so nnz - mask_bits (f3s_bsf_stats) counts the repeated entries.
+ * The masked pass then attends each edge once, whereas the reference's
+ * cpu_sparse_attention_csr (baselines/cpu_baseline.cpp:38-50) counts a
+ * repeated entry once per repeat; the tile-dense pass is unaffected.  Each
+ * call makes one host round trip (to read T and the error bits); scratch
+ * comes from the library's cache. */
 f3s_status f3s_convert_csr_to_bsf(const int32_t* d_row_ptr, const int32_t* d_col_idx,
                                   int32_t n, int64_t nnz,
                                   int32_t* d_window_offsets, int32_t* d_block_col,
@@ -117,7 +129,8 @@ f3s_status f3s_window_order(const int32_t* d_window_offsets, int32_t W,
 /* Figures behind the algorithmic byte model (no reference counterpart):
  * occ_sum = sum over tiles of the columns the fused pass gathers (popcount of
  * the OR of the row masks if d_tile_mask, else the tile's columns < n);
- * mask_bits = popcount of all masks.  Synchronises `stream`. */
+ * mask_bits = popcount of all masks, the distinct edges: mask_bits < nnz iff
+ * the CSR repeats entries.  Synchronises `stream`. */
 f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask,
                          int64_t T, int32_t n, int64_t* occ_sum, int64_t* mask_bits,
                          void* stream);
@@ -152,7 +165,7 @@ f3s_status f3s_bsf_stats(const int32_t* d_block_col, const uint16_t* d_tile_mask
  * (one tile per block column at most) and no team launch is made.  Three
  * small kernels (four given an order; ~15-30 us) build the schedule in
  * scratch of about 9 bytes per window taken from the
- * library's pool and returned to it in stream order on `stream` (the call
+ * library's cache and returned to it in stream order on `stream` (the call
  * does not wait).  Tensors past ~4 GiB take the sequence of the order, as
  * small graphs do.  Every other path allocates nothing. */
 f3s_status f3s_attention_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V,
@@ -250,7 +263,8 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q,
  * columns per step, `cpw` steps per wave: the fused pass's load shape) and
  * folds the bytes into d_out, one word per wave: ceil(count / 32 / cpw)
  * words.  Tables hold `rows` rows (rows * row_stride <= 0xffff0000 bytes);
- * a row past the table reads zero.  Asynchronous on `stream`. */
+ * a negative row or one past the table reads zero.  Asynchronous on
+ * `stream`. */
 f3s_status f3s_probe_gather(const uint16_t* K, const uint16_t* V, int64_t rows,
                             int32_t row_stride, const int32_t* d_idx, int64_t count,
                             int32_t cpw, uint32_t* d_out, void* stream);

@@ -82,7 +82,7 @@ def check_parity(gpu, seed, r, rp, ci, H):
             want = orc.masked_attention(n, 64, H, f(Q), f(K), f(V), rp, ci, scale)
         else:
             want = orc.tile_dense_attention(n, 64, H, f(Q), f(K), f(V), hb.window_offsets,
-                                            hb.block_col_indices, scale)
+                                            hb.block_col_indices, scale, fast=True)
         runs = [(f"unplanned/{k}", None, o, False) for k, o in orders.items()]
         runs += [(f"plan/{k}", 0, o, False) for k, o in orders.items()]
         runs += [("plan/seg", seg, None, False), ("plan/seg/sorted", seg, orders["sorted"], False)]

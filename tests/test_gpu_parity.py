@@ -114,12 +114,13 @@ class Problem:
         hb = self.host_bsf()
         if rows is None:
             return orc.tile_dense_attention(self.n, 64, self.H, self.Qf, self.Kf, self.Vf,
-                                            hb.window_offsets, hb.block_col_indices, scale)
+                                            hb.window_offsets, hb.block_col_indices, scale,
+                                            fast=True)
         out = {}
         for (a, b) in rows:
             out[(a, b)] = orc.tile_dense_attention(self.n, 64, self.H, self.Qf, self.Kf, self.Vf,
                                                    hb.window_offsets, hb.block_col_indices, scale,
-                                                   a, b)[a:b]
+                                                   a, b, fast=True)[a:b]
         return out
 
 
@@ -1026,16 +1027,70 @@ def test_naive_comparator(gpu, case):
     assert np.max(np.abs(got - want)) <= 1e-4
 
 
+# ------------------------------------------------- repeated CSR entries
+
+def test_repeated_csr_entries(gpu):
+    """A CSR that repeats entries (a multigraph).  The reference converter
+    accepts it (its std::set drops the repeats, src/converter.cu:20-29), and
+    so does the drop-in converter: the tile lists and masks are those of the
+    deduplicated CSR, and `duplicate_entries` (= nnz - mask bits, also
+    f3s_bsf_stats') counts the repeats.  As documented, the masked pass then
+    attends each edge once -- it equals the oracle on the deduplicated CSR --
+    whereas cpu_sparse_attention_csr counts every repeat
+    (baselines/cpu_baseline.cpp:38-50), so the rows with repeats differ from
+    the oracle on the multigraph; the tile-dense pass is unaffected."""
+    n = 600
+    rp0, ci0 = random_csr(n, 7, 71)
+    r = rng(72)
+    reps = r.integers(0, len(ci0), 300)            # entries to repeat (some several times)
+    rows0 = np.repeat(np.arange(n), np.diff(rp0))
+    rows = np.concatenate([rows0, rows0[reps]])
+    cols = np.concatenate([ci0, ci0[reps]])
+    key = np.argsort(rows.astype(np.int64) * n + cols, kind="stable")
+    rows, cols = rows[key], cols[key].astype(np.int32)
+    rp = np.zeros(n + 1, np.int64)
+    rp[1:] = np.cumsum(np.bincount(rows, minlength=n))
+    rp = rp.astype(np.int32)
+    dup = len(cols) - len(ci0)
+    assert dup == 300
+    fmt = gpu.convert_csr_to_block_sparse(n, rp, cols, verbose=False)
+    offs, bcol, mask = orc.convert(n, rp0, ci0)
+    assert fmt.duplicate_entries == dup
+    assert np.array_equal(fmt.window_offsets, offs)
+    assert np.array_equal(fmt.block_col_indices, bcol)
+    assert np.array_equal(fmt.tile_masks, mask)
+    # the oracle converter on the multigraph gives the same lists (and masks)
+    offs_m, bcol_m, mask_m = orc.convert(n, rp, cols)
+    assert np.array_equal(offs_m, offs) and np.array_equal(bcol_m, bcol)
+    assert np.array_equal(mask_m, mask)
+    csr = gpu.DeviceCSR(rp, cols)
+    bsf = gpu.convert_device(csr)
+    occ, bits = gpu.bsf_stats(bsf, True)
+    assert bits == len(cols) - dup
+    Q, K, V = (r.uniform(-1, 1, (n, 1, 64)).astype(np.float16) for _ in range(3))
+    Qf, Kf, Vf = (x.astype(np.float32) for x in (Q, K, V))
+    dQ, dK, dV = (gpu.DeviceArray.from_numpy(x.view(np.uint16)) for x in (Q, K, V))
+    dO = gpu.DeviceArray((n, 1, 64), np.float32)
+    for masked in (True, False):
+        dO.fill_bytes(0xFF)
+        gpu.attention_fwd(dQ, dK, dV, dO, bsf, None, masked=masked)
+        gpu.synchronize()
+        got = dO.numpy()
+        if masked:
+            want = orc.masked_attention(n, 64, 1, Qf, Kf, Vf, rp0, ci0)
+            counted_twice = orc.masked_attention(n, 64, 1, Qf, Kf, Vf, rp, cols)
+            rep_rows = np.unique(rows0[reps])
+            assert np.abs(got[rep_rows] - counted_twice[rep_rows]).max() > 10 * ABS_TOL
+            other = np.setdiff1d(np.arange(n), rep_rows)
+            assert np.array_equal(want[other].view(np.uint32),
+                                  counted_twice[other].view(np.uint32))
+        else:
+            want = orc.tile_dense_attention(n, 64, 1, Qf, Kf, Vf, offs, bcol, fast=True)
+        mabs, mrel = errors(got, want)
+        assert mabs <= ABS_TOL and mrel <= REL_TOL, (masked, mabs, mrel)
+
+
 # ------------------------------------------------- full-size configurations
-
-def sample_rows(bsf_host, n, extra_windows=8, stride_rows=4000, seed=0):
-    """Deterministic sample: the heaviest windows plus evenly spaced rows."""
-    cnt = np.diff(bsf_host.window_offsets)
-    heavy = np.argsort(-cnt, kind="stable")[:extra_windows]
-    ranges = [(int(16 * w), int(min(n, 16 * w + 16))) for w in heavy]
-    ranges += [(a, min(n, a + 64)) for a in range(0, n, max(stride_rows, 64))]
-    return ranges
-
 
 def oracle_threads() -> int:
     """Host threads for whole-graph oracle runs (a one-GPU box's CPU share)."""
@@ -1061,17 +1116,6 @@ def check_whole_graph(what: str, got: np.ndarray, want: np.ndarray) -> None:
     log(f"  {what}: every row, max_abs={mabs:.3e} max_rel={mrel:.3e} "
         f"(elementwise rel, |c| >= 0.1: {elem_rel(got, want):.3e})")
     assert mabs <= ABS_TOL and mrel <= REL_TOL, f"{what}: {mabs} {mrel}"
-
-
-def check_sampled(what, got, ranges, want_rows) -> None:
-    assert np.all(np.isfinite(got)), f"{what}: unwritten or non-finite rows"
-    worst = (0.0, 0.0)
-    for (a, b) in ranges:
-        mabs, mrel = errors(got[a:b], want_rows(a, b))
-        assert mabs <= ABS_TOL and mrel <= REL_TOL, f"{what} rows {a}:{b}: {mabs} {mrel}"
-        worst = (max(worst[0], mabs), max(worst[1], mrel))
-    log(f"  {what}: {len(ranges)} row ranges, worst max_abs={worst[0]:.3e} "
-        f"max_rel={worst[1]:.3e}")
 
 
 @pytest.mark.slow
@@ -1127,7 +1171,7 @@ def test_config4_full_size(gpu):
     del want
     t0 = time.time()
     want = orc.tile_dense_attention(n, 64, 1, Qf, Kf, Vf, hb.window_offsets,
-                                    hb.block_col_indices, 1.0, threads=th)
+                                    hb.block_col_indices, 1.0, threads=th, fast=True)
     log(f"cfg4 tile-dense oracle, whole graph: {time.time()-t0:.2f}s on {th} threads")
     for what, fn in (("plan", lambda: plan.forward(dQ, dK, dV, dO, masked=False)),
                      ("drop-in, descending order",
@@ -1139,9 +1183,10 @@ def test_config4_full_size(gpu):
 def test_config5_full_size(gpu):
     """Config 5 at full size (121.9 M edges, 4 heads): the converter in full;
     masked attention on every row for the compiled plan and the drop-in
-    launch in natural order; tile-dense (15.5 TFLOP of tile work for the CPU
-    oracle, minutes on 16 threads) on 608 sampled row ranges of 64 rows
-    (1.6 % of the rows) including the heaviest windows."""
+    launch in natural order; tile-dense attention (15.5 TFLOP of tile work
+    for the CPU oracle's SIMD form, ~25 s on 16 threads) on every row for the
+    plan and for the reference's own launch -- the drop-in f3s_attention_fwd,
+    tile-dense, in the descending order (tests/test_fused_3s_v2.cu:124-153)."""
     c = gpu.CONFIGS[5]
     t0 = time.time()
     rp, ci = c.graph()
@@ -1174,14 +1219,15 @@ def test_config5_full_size(gpu):
                       lambda: gpu.attention_fwd(dQ, dK, dV, dO, bsf, None, masked=True, H=H))):
         check_whole_graph(f"cfg5 masked {what}", run(fn), want)
     del want
-    ranges = sample_rows(hb, n, stride_rows=4000)
-
-    def want_rows(a, b):
-        return orc.tile_dense_attention(n, 64, H, Qf, Kf, Vf, hb.window_offsets,
-                                        hb.block_col_indices, 1.0, a, b, threads=th)[a:b]
-
-    check_sampled("cfg5 tile-dense plan", run(lambda: plan.forward(dQ, dK, dV, dO, masked=False)),
-                  ranges, want_rows)
+    t0 = time.time()
+    want = orc.tile_dense_attention(n, 64, H, Qf, Kf, Vf, hb.window_offsets,
+                                    hb.block_col_indices, 1.0, threads=th, fast=True)
+    log(f"cfg5 tile-dense oracle, whole graph: {time.time()-t0:.2f}s on {th} threads")
+    order = gpu.window_order_device(bsf)
+    for what, fn in (("plan", lambda: plan.forward(dQ, dK, dV, dO, masked=False)),
+                     ("drop-in, descending order",
+                      lambda: gpu.attention_fwd(dQ, dK, dV, dO, bsf, order, masked=False, H=H))):
+        check_whole_graph(f"cfg5 tile-dense {what}", run(fn), want)
 
 
 @pytest.mark.slow
@@ -1194,7 +1240,7 @@ def test_schedule_on_a_graph_of_550_count_blocks(gpu):
     compiled plan (on the same schedule); the drop-in launch in descending
     order (562,500 window-heads: the schedule too) and the allocation-free
     entry point give the natural-order bits, a plan given the order those of
-    a plan without it; tile-dense on sampled rows."""
+    a plan without it; tile-dense on every row."""
     from fused3s_amd import _lib
     n = 9_000_000
     r = rng(97)
@@ -1239,13 +1285,10 @@ def test_schedule_on_a_graph_of_550_count_blocks(gpu):
     assert np.array_equal(got.view(np.uint32), pl.view(np.uint32)), "plan, descending order"
     del got, pl, want
     hb = p.host_bsf()
-    ranges = sample_rows(hb, n, stride_rows=60000)
-
-    def want_rows(a, b):
-        return orc.tile_dense_attention(n, 64, 1, p.Qf, p.Kf, p.Vf, hb.window_offsets,
-                                        hb.block_col_indices, 1.0, a, b, threads=th)[a:b]
-
+    want = orc.tile_dense_attention(n, 64, 1, p.Qf, p.Kf, p.Vf, hb.window_offsets,
+                                    hb.block_col_indices, 1.0, threads=th, fast=True)
     nat = p.run(False)
-    check_sampled("tile-dense drop-in, natural order", nat, ranges, want_rows)
+    check_whole_graph("tile-dense drop-in, natural order", nat, want)
+    del want
     got = p.run(False, order=order)
     assert np.array_equal(got.view(np.uint32), nat.view(np.uint32)), "tile-dense, descending"

@@ -58,6 +58,28 @@ def test_block_sparse_round_trip(tmp_path, n, deg, seed):
     assert same_bsf(bsf, b3, masks=False) and len(b3.tile_masks) == 0
 
 
+def test_repeated_entries_are_counted_on_load(tmp_path):
+    """A multigraph's block-sparse form (the oracle converter's: repeats
+    dropped from the lists and masks) reloads with duplicate_entries =
+    nnz - mask bits."""
+    rp0, ci0 = random_csr(200, 5, 9)
+    n = len(rp0) - 1
+    rows = np.repeat(np.arange(n), np.diff(rp0))
+    extra = np.arange(0, len(ci0), 7)
+    rows2 = np.concatenate([rows, rows[extra]])
+    cols2 = np.concatenate([ci0, ci0[extra]])
+    k = np.argsort(rows2.astype(np.int64) * n + cols2, kind="stable")
+    rows2, cols2 = rows2[k], cols2[k].astype(np.int32)
+    rp = np.zeros(n + 1, np.int32)
+    rp[1:] = np.cumsum(np.bincount(rows2, minlength=n))
+    p = str(tmp_path / "multi.f3sg")
+    f3s.save_graph(p, rp, cols2, oracle_bsf(rp, cols2))
+    g, bsf = f3s.load_graph(p)
+    assert g.num_edges == len(cols2)
+    assert bsf.duplicate_entries == len(extra)
+    assert same_bsf(bsf, oracle_bsf(rp0, ci0))
+
+
 def test_empty_graph(tmp_path):
     p = str(tmp_path / "e.f3sg")
     f3s.save_graph(p, np.zeros(1, np.int32), np.zeros(0, np.int32))

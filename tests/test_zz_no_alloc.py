@@ -79,6 +79,48 @@ def test_noalloc_matches_allocating_entry_point(gpu):
                 assert_close(got, want, what)
 
 
+def test_noalloc_past_512_count_blocks(gpu):
+    """8,500,000 nodes (a self-loop and one more neighbour per row): 531,250
+    windows, so the schedule's class counts span 519 blocks of 1,024 windows,
+    past the 512 that sched_scan keeps in registers -- it takes its two-pass
+    segment loop.  The allocation-free entry point gives f3s_attention_fwd's
+    bits in natural and in descending order, in both semantics, and meets the
+    oracle on sampled rows; then a second, smaller graph through the same
+    scratch gives that entry point's bits too."""
+    from fused3s_amd import _lib
+    lib = _lib.hip()
+    n = 8_500_000
+    i = np.arange(n, dtype=np.int64)
+    j = (i * 7919 + 13) % n
+    two = j != i
+    rp = np.zeros(n + 1, np.int64)
+    rp[1:] = np.cumsum(1 + two)
+    ci = np.empty(int(rp[-1]), np.int32)
+    ci[rp[:-1]] = np.minimum(i, j)
+    ci[rp[:-1][two] + 1] = np.maximum(i, j)[two]
+    p = Problem(gpu, rp.astype(np.int32), ci, H=1, seed=85, f32=True)
+    W = p.bsf.W
+    assert W == 531_250 and -(-W // 1024) > 512
+    order = gpu.window_order_device(p.bsf)
+    ranges = [(a, min(n, a + 64)) for a in range(0, n, n // 24)] + [(n - 40, n)]
+    for masked in (True, False):
+        want = p.oracle(masked, scale=0.125, rows=ranges)
+        nat = call(lib.f3s_attention_fwd, p, masked)
+        for o in (None, order):
+            got = call(lib.f3s_attention_fwd_noalloc, p, masked, o)
+            what = f"noalloc W={W} masked={masked} ordered={o is not None}"
+            assert np.array_equal(got.view(np.uint32), nat.view(np.uint32)), what
+        for (a, b) in ranges:
+            assert_close(nat[a:b], want[(a, b)], f"W={W} masked={masked} rows {a}:{b}")
+    del p, nat, got
+    rp2, ci2 = hub_graph(20000, 86, {5: 20000, 6000: 900})
+    p2 = Problem(gpu, rp2, ci2, H=1, normal=True, seed=86)
+    for masked in (True, False):
+        ref = call(lib.f3s_attention_fwd, p2, masked)
+        got = call(lib.f3s_attention_fwd_noalloc, p2, masked)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), ("second call", masked)
+
+
 def test_noalloc_rejects_graphs_past_its_scratch(gpu):
     from fused3s_amd import _lib
     lib = _lib.hip()
