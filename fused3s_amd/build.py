@@ -7,6 +7,7 @@
   counterpart of the reference's tests/test_fused_3s_v2.cu), when the
   oracle library is present
 * ``oracle/`` via ``make -C oracle`` (test infrastructure)
+* ``tests/cpp/bin/libl2model.so`` -- the L2 cache model of tests/test_l2_bound.py
 
 Run ``python -m fused3s_amd.build``.  Objects go to ``fused3s_amd/_build``.
 """
@@ -140,6 +141,17 @@ def _build_one_harness(name: str, verbose: bool) -> Path | None:
     return out
 
 
+def build_l2_model(verbose: bool = True) -> Path:
+    """The test-side L2 cache model (tests/cpp/l2_model.cpp), a plain shared
+    library for tests/test_l2_bound.py."""
+    bindir = ROOT / "tests" / "cpp" / "bin"
+    bindir.mkdir(parents=True, exist_ok=True)
+    out = bindir / "libl2model.so"
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+          str(ROOT / "tests" / "cpp" / "l2_model.cpp"), "-o", str(out)], verbose)
+    return out
+
+
 def build_all(verbose: bool = True) -> None:
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
@@ -147,6 +159,7 @@ def build_all(verbose: bool = True) -> None:
     build_host(verbose)
     build_oracle(verbose)
     build_harness(verbose)
+    build_l2_model(verbose)
 
 
 if __name__ == "__main__":

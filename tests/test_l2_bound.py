@@ -1,0 +1,264 @@
+"""How far L2 hits could lift config 4's planned masked pass: a bound,
+computed on the CPU.
+
+The pass reads each attended K and V row (one 128-byte line each) where the
+plan puts its item, and the eight XCDs' L2s (4 MB each) do not share lines.
+From the planned pass's own items and their XCDs -- the plan restated from
+attention.hip (plan_count / plan_fill: windows in the descending order, heavy
+windows cut into segments of `seg` tiles) and the launch's mapping (four items
+per workgroup, workgroups dealt to the XCDs round-robin: item i on XCD
+(i / 4) mod 8) -- this builds each XCD's read trace: Q rows at an item's start,
+then per chunk of 32 attended columns its compiled record (two streamed lines),
+the chunk's K rows and its V rows, with 512 items resident per XCD (32 CUs x 4
+workgroups of 4 waves) advancing one chunk per step.  It then counts misses per
+XCD under five policies (tests/cpp/l2_model.cpp): first touch (an L2 of any
+size), Belady's optimum for 4 MB (dead lines not cached; and with bypass),
+16-way LRU (checked against the measured hit rate), the hub rows pinned, and
+LRU over the rows of degree >= 64 only, every other row streaming past the L2
+(a policy a load can choose per row).
+Below-L2 bytes = read misses x 128 + O written (fp32) + split-window partials;
+the largest compulsory-byte fraction a policy allows is the compulsory bytes
+over (its below-L2 bytes / the 7.1 TB/s the pass moves below the L2, measured),
+over the 8 TB/s peak.
+
+CPU only; `python tests/test_l2_bound.py` prints the table as JSON.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import heapq
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "tests"))
+
+import _oracle as orc  # noqa: E402
+
+LIB = ROOT / "tests" / "cpp" / "bin" / "libl2model.so"
+LINE = 128
+L2_LINES = (4 << 20) // LINE          # 4 MB per XCD
+WAYS = 16
+XCDS = 8
+ITEMS_PER_GROUP = 4
+RESIDENT_ITEMS = 32 * 4 * 4           # per XCD: 32 CUs x 4 workgroups x 4 waves
+CHUNK = 32
+BELOW_L2_RATE = 7.1e12                # bytes/s the pass moves below the L2 (profiles/pmc_traffic_cfg4.txt)
+HBM_PEAK = 8.0e12
+MEASURED = {"below_l2_bytes": 3.96e9, "l2_read_hit_rate": 0.196}
+PARTIAL_BYTES = 4224
+HOT_DEGREE = 64                       # selective policy: rows of at least this degree cached
+
+
+def _lib() -> C.CDLL:
+    lib = C.CDLL(str(LIB))
+    i64p = C.POINTER(C.c_int64)
+    lib.l2_first_touch.restype = C.c_int64
+    lib.l2_first_touch.argtypes = [i64p, C.c_int64, C.c_int64]
+    lib.l2_lru.restype = C.c_int64
+    lib.l2_lru.argtypes = [i64p, C.c_int64, C.c_int64, C.c_int32]
+    lib.l2_opt.restype = C.c_int64
+    lib.l2_opt.argtypes = [i64p, C.c_int64, C.c_int64, C.c_int64, C.c_int]
+    lib.l2_lru_selective.restype = C.c_int64
+    lib.l2_lru_selective.argtypes = [i64p, C.c_int64, C.c_int64, C.c_int32,
+                                     C.POINTER(C.c_uint8)]
+    lib.l2_pinned.restype = C.c_int64
+    lib.l2_pinned.argtypes = [i64p, C.c_int64, C.POINTER(C.c_uint8), C.c_int64]
+    return lib
+
+
+def plan_items(offs: np.ndarray, order: np.ndarray, H: int = 1):
+    """The planned pass's items (window, first tile, end tile) in launch
+    order: attention.hip's auto_segments (masked: max(256, 4 mean,
+    ceil(T H / 8192)) tiles) and plan_fill (a window of more than seg tiles
+    becomes ceil(tiles / seg) consecutive segments)."""
+    W = len(offs) - 1
+    T = int(offs[-1])
+    mean = -(-T // W)
+    seg = max(256, 4 * mean, -(-T * H // 8192))
+    tb, te = offs[order].astype(np.int64), offs[order + 1].astype(np.int64)
+    ns = np.where(te - tb > seg, -(-(te - tb) // seg), 1)
+    w = np.repeat(order, ns)
+    k = np.arange(int(ns.sum())) - np.repeat(np.cumsum(ns) - ns, ns)
+    a = np.repeat(tb, ns) + k * seg
+    b = np.minimum(np.repeat(te, ns), a + seg)
+    return w.astype(np.int64), a, b, seg
+
+
+def traces(n: int, offs, bcol, mask, order):
+    """Per XCD: the read trace (line ids: K row r -> r, V row r -> n + r, Q row
+    r -> 2n + r; -1 a streamed record line), plus the figures the byte count
+    needs."""
+    w_it, tb_it, te_it, seg = plan_items(offs, order)
+    nitems = len(w_it)
+    # attended columns of every tile, in tile order (the compiled lists)
+    occ_bits = np.bitwise_or.reduce(mask, axis=1)
+    bits = ((occ_bits[:, None] >> np.arange(16, dtype=np.uint16)) & 1).astype(bool)
+    t_idx, c_idx = np.nonzero(bits)
+    col = bcol[t_idx].astype(np.int64) * 16 + c_idx
+    # tile -> item
+    T = len(bcol)
+    tile_item = np.empty(T, np.int64)
+    for i in range(nitems):   # 63 K items: slice assignment per item
+        tile_item[tb_it[i]:te_it[i]] = i
+    item = tile_item[t_idx]
+    # rank of each column within its item (tiles of an item are contiguous and
+    # in tile order, so the columns of an item are contiguous in t_idx order)
+    first = np.searchsorted(item, np.arange(nitems), side="left") if np.all(np.diff(item) >= 0) \
+        else None
+    if first is None:
+        srt = np.argsort(item, kind="stable")
+        item, col = item[srt], col[srt]
+        first = np.searchsorted(item, np.arange(nitems), side="left")
+    pos = np.arange(len(item)) - first[item]
+    chunk = pos // CHUNK
+    ncols = np.bincount(item, minlength=nitems)
+    nchunks = -(-ncols // CHUNK)
+    # start step of each item on its XCD: list scheduling over RESIDENT_ITEMS
+    # slots, items in launch order, one chunk per step (the Q load: one step)
+    xcd = (np.arange(nitems) // ITEMS_PER_GROUP) % XCDS
+    start = np.zeros(nitems, np.int64)
+    slot = np.zeros(nitems, np.int64)
+    for x in range(XCDS):
+        heap = [(0, s) for s in range(RESIDENT_ITEMS)]
+        for i in np.nonzero(xcd == x)[0]:
+            t, s = heapq.heappop(heap)
+            start[i], slot[i] = t, s
+            heapq.heappush(heap, (t + 1 + int(nchunks[i]), s))
+    out = []
+    for x in range(XCDS):
+        its = np.nonzero(xcd == x)[0]
+        m = xcd[item] == x
+        ci, ck, cc = item[m], chunk[m], col[m]
+        # keys: (step, slot, phase, k); phase 0 Q, 1 record, 2 K, 3 V
+        step_c = start[ci] + 1 + ck
+        keys, ids = [], []
+        # Q rows (16 per item, rows of its window < n)
+        qi = np.repeat(its, 16)
+        qr = np.repeat(w_it[its] * 16, 16) + np.tile(np.arange(16), len(its))
+        keep = qr < n
+        qi, qr = qi[keep], qr[keep]
+        keys.append(((start[qi] * RESIDENT_ITEMS + slot[qi]) * 4 + 0) * 64 + (qr % 16))
+        ids.append(2 * n + qr)
+        # records: two streamed lines per chunk
+        ch_item = np.repeat(its, nchunks[its])
+        ch_k = np.arange(len(ch_item)) - np.repeat(np.cumsum(nchunks[its]) - nchunks[its],
+                                                   nchunks[its])
+        for half in (0, 1):
+            keys.append((((start[ch_item] + 1 + ch_k) * RESIDENT_ITEMS + slot[ch_item]) * 4 + 1)
+                        * 64 + half)
+            ids.append(np.full(len(ch_item), -1, np.int64))
+        base = (step_c * RESIDENT_ITEMS + slot[ci]) * 4
+        keys.append((base + 2) * 64 + pos[m] % CHUNK)
+        ids.append(cc)
+        keys.append((base + 3) * 64 + pos[m] % CHUNK)
+        ids.append(n + cc)
+        k = np.concatenate(keys)
+        v = np.concatenate(ids)
+        srt = np.argsort(k, kind="stable")
+        out.append(np.ascontiguousarray(v[srt], np.int64))
+    nt = np.diff(offs)[order].astype(np.int64)
+    split_slots = int(np.sum(-(-nt[nt > seg] // seg)))
+    return out, {"items": nitems, "seg": seg, "chunks": int(nchunks.sum()),
+                 "split_slots": split_slots}
+
+
+def report(cfgnum: int = 4) -> dict:
+    import fused3s_amd as f3s
+    c = f3s.CONFIGS[cfgnum]
+    assert c.H == 1
+    rp, ci = c.graph()
+    n = c.n
+    offs, bcol, mask = orc.convert(n, rp, ci)
+    order = orc.window_order(offs)
+    tr, info = traces(n, offs, bcol, mask, order)
+    lib = _lib()
+    id_space = 3 * n
+    p64 = C.POINTER(C.c_int64)
+    reads = sum(len(t) for t in tr)
+    res = {"reads_lines": reads}
+    # the hub rows: per XCD, the K and V lines read most often there, as many
+    # as fill its L2
+    pol = {"first_touch": 0, "opt_4MB": 0, "opt_4MB_bypass": 0, "lru_4MB_16way": 0,
+           "pinned_hubs_4MB": 0, "lru_4MB_hot_rows_only": 0}
+    # the policy a load can choose per row: rows of degree >= HOT_DEGREE cached
+    # by LRU, every other K/V row and the Q rows streamed past the L2
+    hot = np.diff(rp) >= HOT_DEGREE
+    cacheable = np.zeros(id_space, np.uint8)
+    cacheable[:n] = hot
+    cacheable[n:2 * n] = hot
+    for t in tr:
+        ptr = t.ctypes.data_as(p64)
+        pol["first_touch"] += lib.l2_first_touch(ptr, len(t), id_space)
+        pol["opt_4MB"] += lib.l2_opt(ptr, len(t), id_space, L2_LINES, 0)
+        pol["opt_4MB_bypass"] += lib.l2_opt(ptr, len(t), id_space, L2_LINES, 1)
+        pol["lru_4MB_16way"] += lib.l2_lru(ptr, len(t), L2_LINES // WAYS, WAYS)
+        pol["lru_4MB_hot_rows_only"] += lib.l2_lru_selective(
+            ptr, len(t), L2_LINES // WAYS, WAYS, cacheable.ctypes.data_as(C.POINTER(C.c_uint8)))
+        kv = t[(t >= 0) & (t < 2 * n)]
+        cnt = np.bincount(kv, minlength=id_space)
+        pinned = np.zeros(id_space, np.uint8)
+        pinned[np.argsort(-cnt, kind="stable")[:L2_LINES]] = 1
+        pol["pinned_hubs_4MB"] += lib.l2_pinned(ptr, len(t),
+                                                pinned.ctypes.data_as(C.POINTER(C.c_uint8)),
+                                                id_space)
+    # bytes below the L2 per pass: read misses, O written, partials
+    kv_rows = int(np.count_nonzero(np.bincount(ci, minlength=n)))
+    writes = n * 64 * 4 + info["split_slots"] * PARTIAL_BYTES * 2
+    compulsory = (n * 128 * 3 + kv_rows * 128 * 2 + info["chunks"] * 256 + info["items"] * 20
+                  + info["split_slots"] * PARTIAL_BYTES * 2)
+    res["compulsory_bytes"] = compulsory
+    res["writes_bytes"] = writes
+    res["policies"] = {}
+    for k, misses in pol.items():
+        below = misses * LINE + writes
+        res["policies"][k] = {
+            "read_misses": int(misses), "read_hit_rate": 1 - misses / reads,
+            "below_l2_bytes": int(below),
+            "max_compulsory_frac": compulsory / (below / BELOW_L2_RATE) / HBM_PEAK}
+    res["measured"] = MEASURED
+    res["model"] = {"hot_degree": HOT_DEGREE, "hot_rows": int(hot.sum()), "xcds": XCDS, "l2_lines_per_xcd": L2_LINES, "resident_items_per_xcd":
+                    RESIDENT_ITEMS, "items": info["items"], "seg": info["seg"],
+                    "chunks": info["chunks"]}
+    return res
+
+
+@pytest.fixture(scope="module")
+def cfg4_report():
+    if not LIB.exists():
+        pytest.skip("tests/cpp/bin/libl2model.so not built (python -m fused3s_amd.build)")
+    return report(4)
+
+
+def test_policies_are_ordered(cfg4_report):
+    """First touch <= Belady with bypass <= Belady <= LRU, and the pinned
+    policy never beats the optimum."""
+    p = {k: v["read_misses"] for k, v in cfg4_report["policies"].items()}
+    assert p["first_touch"] <= p["opt_4MB_bypass"] <= p["opt_4MB"] <= p["lru_4MB_16way"]
+    assert p["opt_4MB_bypass"] <= p["pinned_hubs_4MB"]
+
+
+def test_lru_model_matches_the_measured_pass(cfg4_report):
+    """The model's LRU reproduces the measured pass within 15 %: its below-L2
+    bytes and its L2 read hit rate (3.96 GB, 19.6 %,
+    profiles/pmc_traffic_cfg4.txt)."""
+    lru = cfg4_report["policies"]["lru_4MB_16way"]
+    assert abs(lru["below_l2_bytes"] / MEASURED["below_l2_bytes"] - 1) < 0.15
+    assert abs(lru["read_hit_rate"] - MEASURED["l2_read_hit_rate"]) < 0.15
+
+
+def test_half_of_hbm_peak_is_out_of_reach(cfg4_report):
+    """No L2 policy reaches the 50 % target on this item-to-XCD assignment:
+    not Belady's optimum at 4 MB, and not even an L2 of unlimited size (first
+    touch)."""
+    assert cfg4_report["policies"]["opt_4MB_bypass"]["max_compulsory_frac"] < 0.5
+    assert cfg4_report["policies"]["first_touch"]["max_compulsory_frac"] < 0.5
+
+
+if __name__ == "__main__":
+    print(json.dumps(report(int(sys.argv[1]) if len(sys.argv) > 1 else 4), indent=1))
