@@ -539,10 +539,16 @@ def main() -> int:
     ap.add_argument("--gather-probe", action="store_true",
                     help="only measure the random-gather ceiling (f3s_probe_gather) over "
                          "tables of several sizes and exit")
+    ap.add_argument("--print-source-digests", action="store_true",
+                    help="print the digests of the profiled kernels' sources (the lines a "
+                         "profile under profiles/ records) and exit")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run device-to-device copies of this size (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes) and exit")
     args = ap.parse_args()
+    if args.print_source_digests:
+        print("\n".join(f"sources_{k} {source_digest(k)}" for k in KERNEL_SOURCES))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the path shards "
               "by row-window range with a K/V all-gather, which is not built here.",
@@ -728,6 +734,11 @@ def main() -> int:
     prof = ROOT / "profiles" / f"pmc_traffic_cfg{c.cfg}.txt"
     below = read_profile(prof, "bytes_per_launch") if default_pass else None
     below_us = read_profile(prof, "kernel_avg_us") if default_pass else None
+    # provenance of the traffic figure: the commit and the digest of the
+    # kernel's sources the profile measured, against the sources run here
+    prof_digest = read_profile_field(prof, "sources_fused_attention") if below else None
+    prof_commit = read_profile_field(prof, "commit") if below else None
+    digest_now = source_digest("fused_attention")
     res = {
         "metric": "fused attention edges/s + kernel us; achieved HBM GB/s (% of peak) on 1 MI355X",
         "value": nnz * args.steps / wall,
@@ -759,7 +770,11 @@ def main() -> int:
                                      "(copy-calibrated): traffic below the L2, HBM or the 256 MB "
                                      "Infinity Cache (no gfx950 counter separates them); read "
                                      "from the committed profile of this workload",
-                     "traffic_source": str(prof.relative_to(ROOT)) if below else None},
+                     "traffic_source": str(prof.relative_to(ROOT)) if below else None,
+                     "traffic_commit": prof_commit,
+                     "traffic_sources_digest": prof_digest,
+                     "sources_digest_now": digest_now,
+                     "traffic_sources_current": (prof_digest == digest_now) if below else None},
         "gather_model": {"bytes_per_launch": gbytes, "GBps": gbytes / (kavg * 1e-3) / 1e9,
                          "note": "every gathered K/V row counted once per attending tile "
                                  "(the survey's model); L2 and the Infinity Cache serve part "
