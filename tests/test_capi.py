@@ -169,3 +169,50 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def _bench():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench_mod", ROOT / "bench.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_bench_checker_flags_errors_and_unwritten_rows():
+    """bench.py's row checker: the north star's bounds (2e-3 abs, 1e-2
+    normwise rel), a NaN (an unwritten row) always fails, an exact copy
+    passes with zero error."""
+    b = _bench()
+    want = np.random.default_rng(3).standard_normal((1000, 2, 64)).astype(np.float32)
+    ok = b.compare_rows(want.copy(), want)
+    assert ok["ok"] and ok["max_abs"] == 0.0 and ok["rows"] == "every row"
+    near = want.copy()
+    near[7, 1, 3] += 1.5e-3
+    assert b.compare_rows(near, want)["ok"]
+    far = want.copy()
+    far[999, 0, 63] += 3e-3
+    r = b.compare_rows(far, want)
+    assert not r["ok"] and abs(r["max_abs"] - 3e-3) < 1e-6
+    nan = want.copy()
+    nan[500] = np.nan
+    r = b.compare_rows(nan, want)
+    assert not r["ok"] and r["non_finite"] == 128
+
+
+def test_profiles_record_their_sources():
+    """Every committed profile names the commit it measured and the digests
+    of the kernel sources; bench.py reads them, and --print-source-digests
+    prints the current ones in the same form."""
+    b = _bench()
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--print-source-digests"],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0
+    now = dict(line.split() for line in r.stdout.splitlines())
+    assert set(now) == {f"sources_{k}" for k in b.KERNEL_SOURCES}
+    for prof in sorted((ROOT / "profiles").glob("*.txt")):
+        commit = b.read_profile_field(prof, "commit")
+        assert commit and len(commit) >= 7, prof.name
+        for k in b.KERNEL_SOURCES:
+            d = b.read_profile_field(prof, f"sources_{k}")
+            assert d and len(d) == 16, (prof.name, k)
