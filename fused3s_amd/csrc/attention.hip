@@ -289,6 +289,22 @@ fused_attention_kernel(const AttnParams p)
       }
     } else {
         // ---- tile-dense path: two whole tiles (32 contiguous columns) per chunk ----
+        // Far tiles stream past the L2 when at least a quarter of the item's
+        // tiles are near (kNearCols); one-wave items of the narrow path only.
+        bool stream_far = false;
+        if constexpr (!WIDE && TEAM == 1) {
+            int64_t near = 0;
+            for (int32_t t0 = tb; t0 < te; t0 += kWave) {
+                const int32_t t = t0 + lane;
+                bool is_near = false;
+                if (t < te) {
+                    const int32_t bc = block_col[t];
+                    is_near = bc >= w - kNearCols && bc <= w + kNearCols;
+                }
+                near += __popcll(__ballot(is_near));
+            }
+            stream_far = 4 * near >= (int64_t)(te - tb);
+        }
         for (int32_t t = tb; t < te; t += 2) {
             const int32_t bc0 = block_col[t];
             const int32_t bc1 = (t + 1 < te) ? block_col[t + 1] : -1;
@@ -298,13 +314,50 @@ fused_attention_kernel(const AttnParams p)
                 return ok && c + s < n ? (uint32_t)(c + s) * ref_stride : no_ref;
             };
             h8 krow[4], vrow[4];
+            uint32_t ref[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int s = (lane >> 3) + 8 * i;   // slots 0-15: tile t, 16-31: tile t+1
-                const uint32_t ref = s < 16 ? row_at(ok0, c0, s) : row_at(ok1, c1, s - 16);
-                const uint32_t extra = head_off + 16 * (lane & 7);
-                krow[i] = load_ref<WIDE>(kres, p.K, ref, row_stride, extra);
-                vrow[i] = load_ref<WIDE>(vres, p.V, ref, row_stride, extra);
+                ref[i] = s < 16 ? row_at(ok0, c0, s) : row_at(ok1, c1, s - 16);
+            }
+            const uint32_t extra = head_off + 16 * (lane & 7);
+            // wave-uniform: loads 0-1 belong to tile t, loads 2-3 to tile t+1
+            const bool far0 = stream_far && (bc0 < w - kNearCols || bc0 > w + kNearCols);
+            const bool far1 = stream_far && (bc1 < w - kNearCols || bc1 > w + kNearCols);
+            if (!far0 && !far1) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    krow[i] = load_ref<WIDE>(kres, p.K, ref[i], row_stride, extra);
+                    vrow[i] = load_ref<WIDE>(vres, p.V, ref[i], row_stride, extra);
+                }
+            } else if (far0 && far1) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    krow[i] = load_h8<kStreamLoad>(kres, ref[i] + extra);
+                    vrow[i] = load_h8<kStreamLoad>(vres, ref[i] + extra);
+                }
+            } else if (far0) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    krow[i] = load_h8<kStreamLoad>(kres, ref[i] + extra);
+                    vrow[i] = load_h8<kStreamLoad>(vres, ref[i] + extra);
+                }
+#pragma unroll
+                for (int i = 2; i < 4; ++i) {
+                    krow[i] = load_h8<0>(kres, ref[i] + extra);
+                    vrow[i] = load_h8<0>(vres, ref[i] + extra);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    krow[i] = load_h8<0>(kres, ref[i] + extra);
+                    vrow[i] = load_h8<0>(vres, ref[i] + extra);
+                }
+#pragma unroll
+                for (int i = 2; i < 4; ++i) {
+                    krow[i] = load_h8<kStreamLoad>(kres, ref[i] + extra);
+                    vrow[i] = load_h8<kStreamLoad>(vres, ref[i] + extra);
+                }
             }
             // logit j of the lane is column 4g + j of tile t (j < 4) or
             // 4g + j - 4 of tile t+1; attended iff the column exists
