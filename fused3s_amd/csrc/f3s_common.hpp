@@ -58,9 +58,6 @@ void dev_free_idle(void* ptr, int device);
 // Waits for every stream of `device`, then returns `ptr` for reuse: for
 // memory whose last users may be on any stream (hipFree's behaviour).
 void dev_free_synced(void* ptr, int device);
-// dev_free_synced for caller-owned memory (f3s_free): blocks of 64 MiB and
-// more go back to the driver (hipFree), smaller ones to the cache.
-void dev_free_to_driver_if_large(void* ptr, int device);
 // Host-pinned staging words of the calling thread (16 x int64), for the small
 // device-to-host reads of counts and status that size outputs.
 int64_t* host_staging();

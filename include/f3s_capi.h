@@ -75,8 +75,8 @@ f3s_status f3s_device_name(char* buf, int32_t buflen);
  * allocation (0 keeps nothing); on an allocation failure the cache goes back
  * to the driver and the allocation is retried.  f3s_malloc'd memory is usable
  * on every stream on return; f3s_free waits for the device first, as hipFree
- * does, and returns blocks of 64 MiB and more to the driver at once (smaller
- * ones to the cache). */
+ * does, and returns the block to the cache (f3s_release_cached_memory hands
+ * every idle block back to the driver). */
 f3s_status f3s_malloc(void** ptr, uint64_t bytes);
 f3s_status f3s_free(void* ptr);
 /* Returns every idle cached block to the driver (waits for every device
