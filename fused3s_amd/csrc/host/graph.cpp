@@ -113,11 +113,19 @@ void save_graph_binary(const std::string& path, const GraphData& g, const blockS
         throw std::runtime_error(f3s_host_last_error());
 }
 
-// Distinct (row, column) pairs the masks record.
+// Distinct (row, column) pairs the masks record (a tile's 16 masks are 32
+// bytes, so the array is a whole number of 64-bit words).
 static int64_t mask_popcount(const std::vector<uint16_t>& masks)
 {
     int64_t bits = 0;
-    for (uint16_t m : masks) bits += __builtin_popcount(m);
+    const size_t words = masks.size() / 4;
+    const unsigned char* b = reinterpret_cast<const unsigned char*>(masks.data());
+    for (size_t i = 0; i < words; ++i) {
+        uint64_t x;
+        memcpy(&x, b + 8 * i, sizeof x);
+        bits += __builtin_popcountll(x);
+    }
+    for (size_t i = 4 * words; i < masks.size(); ++i) bits += __builtin_popcount(masks[i]);
     return bits;
 }
 
@@ -178,6 +186,11 @@ blockSparseFormat convert_csr_to_block_sparse(int num_nodes, const std::vector<i
                                  (int32_t*)offs.p, (int32_t*)bcol.p, (uint16_t*)mask.p, &T2,
                                  nullptr),
           "f3s_convert_csr_to_bsf (fill)");
+    // the distinct (row, column) pairs, counted on the device
+    int64_t occ = 0, mask_bits = 0;
+    check(f3s_bsf_stats((const int32_t*)bcol.p, (const uint16_t*)mask.p, T, num_nodes, &occ,
+                        &mask_bits, nullptr),
+          "f3s_bsf_stats");
     bsf.window_offsets.resize((size_t)W + 1);
     bsf.block_col_indices.resize((size_t)T);
     bsf.tile_masks.resize((size_t)T * 16);
@@ -188,7 +201,7 @@ blockSparseFormat convert_csr_to_block_sparse(int num_nodes, const std::vector<i
               "d2h");
         check(f3s_memcpy_d2h(bsf.tile_masks.data(), mask.p, 32 * (size_t)T, nullptr), "d2h");
     }
-    bsf.duplicate_entries = nnz - mask_popcount(bsf.tile_masks);
+    bsf.duplicate_entries = nnz - mask_bits;
     std::cout << "Row Windows: " << bsf.num_row_windows << std::endl;
     std::cout << "Total Active Blocks: " << bsf.block_col_indices.size() << std::endl;
     if (bsf.duplicate_entries > 0)

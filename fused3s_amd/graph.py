@@ -41,7 +41,7 @@ class BlockSparseFormat:
 
 def _mask_bits(masks: np.ndarray) -> int:
     """Distinct (row, column) pairs the row masks record."""
-    return int(np.unpackbits(np.ascontiguousarray(masks, np.uint16).view(np.uint8)).sum())
+    return int(np.bitwise_count(np.ascontiguousarray(masks, np.uint16)).sum(dtype=np.int64))
 
 
 def _take_i32(ptr, count: int) -> np.ndarray:
@@ -169,8 +169,10 @@ def convert_csr_to_block_sparse(num_nodes: int, row_ptr, col_ind, verbose: bool 
     col_ind = np.asarray(col_ind, np.int32)
     if len(row_ptr) != num_nodes + 1:
         raise ValueError("convert_csr_to_block_sparse: row_ptr must hold n+1 entries")
-    bsf = convert_device(DeviceCSR(row_ptr, col_ind)).to_host()
-    bsf.duplicate_entries = len(col_ind) - _mask_bits(bsf.tile_masks)
+    dev = convert_device(DeviceCSR(row_ptr, col_ind))
+    _, mask_bits = bsf_stats(dev, True)   # the distinct (row, column) pairs, on the device
+    bsf = dev.to_host()
+    bsf.duplicate_entries = len(col_ind) - mask_bits
     if verbose:
         print(f"Row Windows: {bsf.num_row_windows}")
         print(f"Total Active Blocks: {len(bsf.block_col_indices)}")
