@@ -19,6 +19,9 @@
 //     out in coalesced stores.  Each workgroup keeps the loads of its next
 //     window in flight while it works on the current one, and its barriers
 //     order LDS only, so they do not wait for those loads;
+//   * count_waves: the count pass of graphs whose bitmap is small (W <=
+//     65,536 windows): one window per wave with a bitmap of its own, no
+//     workgroup barrier;
 //   * convert_hubs: the windows with more edges (listed by convert_light),
 //     one 1024-thread workgroup each -- or, on graphs too wide for one
 //     bitmap, every window with 256 threads, the bitmap swept in column
@@ -843,6 +846,166 @@ convert_light(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ c
     if (tid == 0 && *L.bad) atomicOr(err, kErrCol);
 }
 
+// ---------------------------------------------------------------------------
+// count_waves: the count pass of graphs whose bitmap is small (W <=
+// 32 * kWaveCountMaxWords windows): one window per wave, each wave with a
+// bitmap of its own in LDS, so a window costs no workgroup barrier.  A wave
+// takes windows w, w + GW, w + 2 GW, ... (GW waves in the grid); while it
+// marks one window, the columns of its next window and the row pointers of
+// the one after are in flight.  Its counts leave 64 windows at a time (lane
+// k keeps the count of the batch's k-th window): gfx950 counts loads and
+// stores with one counter, so a store pending at every window would make
+// each wait a wait for the prefetched loads too.  Windows of more than
+// kLightEdges edges are listed for convert_hubs, which writes their counts
+// (the zero this pass leaves there is overwritten).  Same counts, same hub
+// list and same error bits as convert_light<false>; on graphs of many block
+// columns the bitmap per wave leaves fewer windows in flight per CU than
+// convert_light's shared one, which is used there.
+// ---------------------------------------------------------------------------
+constexpr int kWaveCountWaves = 4;                   // waves per workgroup
+constexpr int kWaveCountEPL = kLightEdges / kWave;   // edge slots per lane
+constexpr int32_t kWaveCountMaxWords = 2048;         // 8 KB of bitmap per wave
+
+struct WaveWin {
+    int32_t e0, E;
+    bool ok;   // row pointers usable
+};
+
+// Row pointers of window wn: lane t <= nrows holds row_ptr[16 wn + t]; the
+// other lanes (and every lane past the last window) load past the end of
+// the descriptor `rp` over row_ptr[0..n], which reads 0 -- one unconditional
+// load, so nothing waits for it before its value is used.
+__device__ __forceinline__ int32_t wave_fetch_rp(__amdgpu_buffer_rsrc_t rp, int32_t n, int32_t W,
+                                                 int64_t wn, int lane)
+{
+    uint32_t off = 4u * ((uint32_t)n + 1u);   // out of range
+    if (wn < W) {
+        const int nrows = min(16, n - (int32_t)wn * 16);
+        if (lane <= nrows) off = 4u * (uint32_t)(wn * 16 + lane);
+    }
+    return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0);
+}
+
+// The window's edge range, and whether its row pointers are usable (0 <=
+// rp[0] <= ... <= rp[nrows] <= nnz), from the fetched row pointers; all
+// wave-uniform (scalar).
+__device__ __forceinline__ WaveWin wave_describe(int32_t v, int32_t n, int64_t nnz, int64_t wn,
+                                                 int32_t W, int lane)
+{
+    WaveWin d{0, 0, false};
+    if (wn >= W) return d;
+    const int nrows = min(16, n - (int32_t)wn * 16);
+    const int32_t rp0 = __builtin_amdgcn_readfirstlane(__shfl(v, 0, kWave));
+    const int32_t rpn = __builtin_amdgcn_readfirstlane(__shfl(v, nrows, kWave));
+    const int32_t nxt = __shfl_down(v, 1, kWave);
+    const bool back = lane < nrows && nxt < v;
+    d.ok = !__any(back) && rp0 >= 0 && rpn >= rp0 && (int64_t)rpn <= nnz;
+    d.e0 = rp0;
+    d.E = d.ok ? rpn - rp0 : 0;
+    return d;
+}
+
+// Issues the loads of a light window's columns: edge lane + 64 j in col[j],
+// through a buffer descriptor over the window's edges (32-bit offsets; a
+// load past them reads 0 and touches no memory).  The values are not used
+// here, so the loads stay in flight.
+__device__ __forceinline__ void wave_issue_cols(const WaveWin& d,
+                                                const int32_t* __restrict__ col_idx, int lane,
+                                                int32_t (&col)[kWaveCountEPL])
+{
+    const int32_t E = d.E <= kLightEdges ? d.E : 0;   // hubs and unusable windows: none
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(col_idx) + (E > 0 ? d.e0 : 0), (short)0, 4 * E, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < kWaveCountEPL; ++j)
+        col[j] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * (lane + kWave * j), 0, 0);
+}
+
+__global__ void __launch_bounds__(kWaveCountWaves * kWave)
+count_waves(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_idx, int32_t n,
+            int64_t nnz, int32_t W, int32_t* __restrict__ counts, int32_t* __restrict__ hubs,
+            int32_t* __restrict__ num_hubs, int32_t* __restrict__ err)
+{
+    const int words = (W + 31) / 32;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    uint32_t* bits = reinterpret_cast<uint32_t*>(conv_lds) + (size_t)wave * words;
+    for (int i = lane; i < words; i += kWave) bits[i] = 0u;
+    F3S_WAVE_LDS_SYNC();
+    const int64_t GW = (int64_t)gridDim.x * kWaveCountWaves;
+    int64_t w = (int64_t)blockIdx.x * kWaveCountWaves + wave;
+    if (w >= W) return;   // wave-uniform; the kernel has no workgroup barrier
+
+    bool bad = false;           // a column outside [0, n) was seen
+    int32_t mycount = 0;        // count of the batch's lane-th window
+    int nb = 0;                 // windows in the batch
+    int64_t wfirst = w;         // the batch's first window
+    // Marks window wn's columns, leaves the bitmap clear again and returns
+    // its tile count (0 for an unusable, empty or hub window).
+    auto process = [&](const WaveWin& d, int64_t wn, const int32_t (&col)[kWaveCountEPL]) {
+        int32_t cnt = 0;
+        if (!d.ok) {
+            if (lane == 0) atomicOr(err, kErrRowPtr);
+        } else if (d.E > kLightEdges) {
+            if (lane == 0) hubs[atomicAdd(num_hubs, 1)] = (int32_t)wn;
+        } else if (d.E > 0) {
+            int fresh = 0;
+#pragma unroll
+            for (int j = 0; j < kWaveCountEPL; ++j) {
+                const int32_t c = col[j];
+                if (lane + kWave * j < d.E) {
+                    if (c < 0 || c >= n) {
+                        bad = true;
+                    } else {
+                        const uint32_t bit = 1u << ((c >> 4) & 31);
+                        fresh += (atomicOr(&bits[c >> 9], bit) & bit) == 0u;
+                    }
+                }
+            }
+            cnt = wave_sum(fresh);
+            F3S_WAVE_LDS_SYNC();   // every mark is done before the clears
+#pragma unroll
+            for (int j = 0; j < kWaveCountEPL; ++j) {
+                const int32_t c = col[j];
+                if (lane + kWave * j < d.E && c >= 0 && c < n) bits[c >> 9] = 0u;
+            }
+            F3S_WAVE_LDS_SYNC();
+        }
+        if (lane == nb) mycount = cnt;
+        if (++nb == kWave) {
+            counts[wfirst + lane * GW] = mycount;
+            nb = 0;
+            wfirst = wn + GW;
+        }
+    };
+
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int32_t*>(row_ptr), (short)0, (int32_t)(4 * ((int64_t)n + 1)), 0x00020000);
+    int32_t colA[kWaveCountEPL], colB[kWaveCountEPL];
+    WaveWin dA = wave_describe(wave_fetch_rp(rp, n, W, w, lane), n, nnz, w, W, lane);
+    int32_t rpN = wave_fetch_rp(rp, n, W, w + GW, lane);   // next window, in flight
+    wave_issue_cols(dA, col_idx, lane, colA);
+    WaveWin dB;
+    // Two windows per trip so that the two column register sets alternate
+    // without copies (a copy would wait for the loads in flight).
+    while (true) {
+        dB = wave_describe(rpN, n, nnz, w + GW, W, lane);
+        wave_issue_cols(dB, col_idx, lane, colB);
+        rpN = wave_fetch_rp(rp, n, W, w + 2 * GW, lane);
+        process(dA, w, colA);
+        w += GW;
+        if (w >= W) break;
+        dA = wave_describe(rpN, n, nnz, w + GW, W, lane);
+        wave_issue_cols(dA, col_idx, lane, colA);
+        rpN = wave_fetch_rp(rp, n, W, w + 2 * GW, lane);
+        process(dB, w, colB);
+        w += GW;
+        if (w >= W) break;
+    }
+    if (lane < nb) counts[wfirst + lane * GW] = mycount;
+    if (__any(bad) && lane == 0) atomicOr(err, kErrCol);
+}
+
 // Hub windows heaviest first.  convert_light lists them in the order its
 // workgroups find them; rank_hubs writes the list again, ordered by
 // descending edge count (ties: ascending window index, so the order is
@@ -1007,17 +1170,29 @@ static f3s_status launch_pass(const int32_t* row_ptr, const int32_t* col_idx, in
         F3S_HIP(hipGetLastError());
         return F3S_OK;
     }
-    const LightLayout lay = light_layout(W, FILL);
     int dev = 0, cus = 0, per_cu = 0;
     F3S_HIP(hipGetDevice(&dev));
     F3S_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, convert_light<FILL>,
-                                                         kConvThreads, lay.bytes));
-    const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
-    const unsigned grid = (unsigned)(W < resident ? W : resident);
-    hipLaunchKernelGGL((convert_light<FILL>), dim3(grid), dim3(kConvThreads), lay.bytes, stream,
-                       row_ptr, col_idx, n, nnz, W, counts, window_offsets, block_col,
-                       tile_mask, hubs, num_hubs, err);
+    if (!FILL && (int64_t)W <= 32LL * kWaveCountMaxWords) {
+        // small bitmap: the count pass with one window per wave
+        const uint32_t lds = (uint32_t)(sizeof(uint32_t) * kWaveCountWaves * ((W + 31) / 32));
+        F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, count_waves,
+                                                             kWaveCountWaves * kWave, lds));
+        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+        const int64_t need = ceil_div(W, kWaveCountWaves);
+        hipLaunchKernelGGL(count_waves, dim3((unsigned)(need < resident ? need : resident)),
+                           dim3(kWaveCountWaves * kWave), lds, stream, row_ptr, col_idx, n, nnz,
+                           W, counts, hubs, num_hubs, err);
+    } else {
+        const LightLayout lay = light_layout(W, FILL);
+        F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, convert_light<FILL>,
+                                                             kConvThreads, lay.bytes));
+        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+        const unsigned grid = (unsigned)(W < resident ? W : resident);
+        hipLaunchKernelGGL((convert_light<FILL>), dim3(grid), dim3(kConvThreads), lay.bytes,
+                           stream, row_ptr, col_idx, n, nnz, W, counts, window_offsets, block_col,
+                           tile_mask, hubs, num_hubs, err);
+    }
     F3S_HIP(hipGetLastError());
     const int32_t rank_wgs = (int32_t)ceil_div(W < kHubSortCap ? W : kHubSortCap, 64);
     hipLaunchKernelGGL(rank_hubs, dim3((unsigned)rank_wgs), dim3(256), 0, stream, row_ptr, n, W,
