@@ -35,8 +35,8 @@
 //   (scale_fragment_by_row, src/fused3s_v2.cu:54-71) is a plain multiply by
 //   the lane's own correction: no shuffles, no LDS round trip for P.
 //   Q stays in registers in B-operand layout for the whole item.
-//   Segments of split windows write (m, l, O) partials; merge_partials_kernel
-//   combines them in slot order in a second, small launch.
+//   Segments of split windows write (m, l, O) partials; the last segment of
+//   a window to finish combines them in slot order, in the same launch.
 //
 // MFMA 16x16x32 f16 operand layout used (CDNA3/CDNA4 16x16 family): lane l
 // supplies row l%16 of A and column l%16 of B, 8 consecutive k per lane in
@@ -65,6 +65,83 @@ enum Mode : int {
     kModeList = 1,    // masked, compiled column lists (planned + compiled)
     kModeDense = 2,   // tile-dense semantics
 };
+
+// Combines the partials of split window `si` for head h, in slot order
+// (deterministic): M = max m_k, O = sum O_k 2^(m_k - M) / sum l_k 2^(m_k - M),
+// and writes its O rows.  Lane (g, r) owns row r, dims 16g..16g+15.  An
+// online merge over the segments, KB segments' loads in flight at a time:
+// (m, l, O) of a batch are rescaled to the batch's running max, so one pass
+// suffices.  The partials were written through to memory by segments that
+// may have run on other XCDs, and are read the same way (kCoherent).
+template <int KB>
+__device__ __forceinline__ void merge_split(const AttnParams& p, const SplitInfo si, int h,
+                                            int lane)
+{
+    const int H = p.H;
+    const int g = lane >> 4, r = lane & 15;
+    float M = -INFINITY, Ls = 0.f;
+    float4 o[4] = {make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0),
+                   make_float4(0, 0, 0, 0)};
+    for (int k0 = 0; k0 < si.nseg; k0 += KB) {
+        float mk[KB], lk[KB];
+        float4 a[KB][4];
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            const bool in = k0 + j < si.nseg;
+            // one descriptor per partial: 32-bit offsets inside it
+            const float* pk =
+                p.partials + ((int64_t)(si.first_slot + (in ? k0 + j : k0)) * H + h) * kPartialFloats;
+            const __amdgpu_buffer_rsrc_t pr = make_rsrc(pk, sizeof(float) * kPartialFloats);
+            mk[j] = in ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                             pr, sizeof(float) * (16 * kD + r), 0, kCoherent))
+                       : -INFINITY;
+            lk[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                pr, sizeof(float) * (16 * kD + 16 + r), 0, kCoherent));
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const u4 x = __builtin_amdgcn_raw_buffer_load_b128(
+                    pr, sizeof(float) * (r * kD + 16 * g + 4 * v), 0, kCoherent);
+                a[j][v] = make_float4(__uint_as_float(x.x), __uint_as_float(x.y),
+                                      __uint_as_float(x.z), __uint_as_float(x.w));
+            }
+        }
+        float Mb = M;
+#pragma unroll
+        for (int j = 0; j < KB; ++j) Mb = __builtin_fmaxf(Mb, mk[j]);
+        if (Mb == -INFINITY) continue;   // all rows of these segments empty
+        const float c = fast_exp2(M - Mb);   // 0 while M is still -inf
+        Ls *= c;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            o[v].x *= c;
+            o[v].y *= c;
+            o[v].z *= c;
+            o[v].w *= c;
+        }
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            const float f = fast_exp2(mk[j] - Mb);   // 0 for absent / empty segments
+            Ls += lk[j] * f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                o[v].x += a[j][v].x * f;
+                o[v].y += a[j][v].y * f;
+                o[v].z += a[j][v].z * f;
+                o[v].w += a[j][v].w * f;
+            }
+        }
+        M = Mb;
+    }
+    const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+    const int32_t row = si.w * 16 + r;
+    if (row < p.n) {
+        float* dst = p.O + ((int64_t)row * H + h) * kD + 16 * g;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            *reinterpret_cast<float4*>(dst + 4 * v) =
+                make_float4(o[v].x * inv, o[v].y * inv, o[v].z * inv, o[v].w * inv);
+    }
+}
 
 // The pass is bound by memory throughput, not latency: keeping a second
 // chunk's gathers in flight per wave (double-buffered registers, 3 waves per
@@ -435,92 +512,40 @@ fused_attention_kernel(const AttnParams p)
         }
         return;
     }
-    // Segment of a split window: publish (m, l, unnormalised O) for the merge.
-    float* part = p.partials + ((int64_t)slot * H + h) * kPartialFloats;
-    float* op = part + r * kD + 16 * g;
+    // Segment of a split window: its (m, l, unnormalised O) goes through to
+    // memory; once every store of the wave is done (vmcnt(0)) the segment
+    // counts itself in, and the last of the window's segments to do so
+    // merges all of them (its own included, from memory) and leaves the
+    // count at zero for the next pass.  The count's atomics are coherent
+    // across XCDs.
+    const int32_t sid = p.slot_split[slot];
+    const SplitInfo si = p.splits[sid];
+    const __amdgpu_buffer_rsrc_t pres =
+        make_rsrc(p.partials + ((int64_t)slot * H + h) * kPartialFloats,
+                  sizeof(float) * kPartialFloats);
 #pragma unroll
     for (int v = 0; v < 4; ++v)
-        *reinterpret_cast<float4*>(op + 4 * v) =
-            make_float4(st.acc[0][v], st.acc[1][v], st.acc[2][v], st.acc[3][v]);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u4{__float_as_uint(st.acc[0][v]), __float_as_uint(st.acc[1][v]),
+               __float_as_uint(st.acc[2][v]), __float_as_uint(st.acc[3][v])},
+            pres, (uint32_t)(sizeof(float) * (r * kD + 16 * g + 4 * v)), 0, kCoherent);
     if (g == 0) {
-        part[16 * kD + r] = st.m;
-        part[16 * kD + 16 + r] = lrow;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(st.m), pres,
+                                              (uint32_t)(sizeof(float) * (16 * kD + r)), 0,
+                                              kCoherent);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lrow), pres,
+                                              (uint32_t)(sizeof(float) * (16 * kD + 16 + r)), 0,
+                                              kCoherent);
     }
-}
-
-// Combines the segments of each split window, in slot order (deterministic):
-// M = max m_k, O = sum O_k 2^(m_k - M) / sum l_k 2^(m_k - M).  One wave per
-// (split window, head); lane (g, r) owns row r, dims 16g..16g+15.
-__global__ void __launch_bounds__(256) merge_partials_kernel(const AttnParams p)
-{
-    const int H = p.H;
-    const uint32_t gw = blockIdx.x * 4u + threadIdx.x / kWave;
-    const int lane = threadIdx.x % kWave;
-    const int g = lane >> 4, r = lane & 15;
-    const int64_t sid = (int64_t)(gw / (uint32_t)H);
-    const int h = (int)(gw % (uint32_t)H);
-    if (sid >= p.num_split) return;
-    const SplitInfo si = p.splits[sid];
-    auto part = [&](int k) {
-        return p.partials + ((int64_t)(si.first_slot + k) * H + h) * kPartialFloats;
-    };
-    // Online merge over the segments in slot order, eight segments' loads in
-    // flight at a time: a small graph's merge is otherwise a chain of
-    // dependent load latencies.  (m, l, O) of a batch are rescaled to the
-    // batch's running max, so one pass suffices.
-    float M = -INFINITY, Ls = 0.f;
-    float4 o[4] = {make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0), make_float4(0, 0, 0, 0),
-                   make_float4(0, 0, 0, 0)};
-    constexpr int kB = 8;
-    for (int k0 = 0; k0 < si.nseg; k0 += kB) {
-        float mk[kB], lk[kB];
-        float4 a[kB][4];
-#pragma unroll
-        for (int j = 0; j < kB; ++j) {
-            const bool in = k0 + j < si.nseg;
-            const float* pk = part(in ? k0 + j : k0);
-            mk[j] = in ? pk[16 * kD + r] : -INFINITY;
-            lk[j] = pk[16 * kD + 16 + r];
-            const float* src = pk + r * kD + 16 * g;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) a[j][v] = *reinterpret_cast<const float4*>(src + 4 * v);
-        }
-        float Mb = M;
-#pragma unroll
-        for (int j = 0; j < kB; ++j) Mb = __builtin_fmaxf(Mb, mk[j]);
-        if (Mb == -INFINITY) continue;   // all rows of these segments empty
-        const float c = fast_exp2(M - Mb);   // 0 while M is still -inf
-        Ls *= c;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            o[v].x *= c;
-            o[v].y *= c;
-            o[v].z *= c;
-            o[v].w *= c;
-        }
-#pragma unroll
-        for (int j = 0; j < kB; ++j) {
-            const float f = fast_exp2(mk[j] - Mb);   // 0 for absent / empty segments
-            Ls += lk[j] * f;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                o[v].x += a[j][v].x * f;
-                o[v].y += a[j][v].y * f;
-                o[v].z += a[j][v].z * f;
-                o[v].w += a[j][v].w * f;
-            }
-        }
-        M = Mb;
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    int32_t* cnt = p.counters + (int64_t)sid * H + h;
+    int last = 0;
+    if (lane == 0) {
+        last = atomicAdd(cnt, 1) == si.nseg - 1;
+        if (last) atomicExch(cnt, 0);
     }
-    const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
-    const int32_t row = si.w * 16 + r;
-    if (row < p.n) {
-        float* dst = p.O + ((int64_t)row * H + h) * kD + 16 * g;
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-            *reinterpret_cast<float4*>(dst + 4 * v) =
-                make_float4(o[v].x * inv, o[v].y * inv, o[v].z * inv, o[v].w * inv);
-    }
+    if (!__shfl(last, 0, kWave)) return;
+    merge_split<2>(p, si, h, lane);
 }
 
 __global__ void warm_attention_kernel() {}
@@ -902,7 +927,7 @@ __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __res
                           const int64_t* __restrict__ item_base,
                           const int64_t* __restrict__ slot_base,
                           const int64_t* __restrict__ split_base, Item* __restrict__ items,
-                          SplitInfo* __restrict__ splits)
+                          SplitInfo* __restrict__ splits, int32_t* __restrict__ slot_split)
 {
     const int32_t L = blockIdx.x * blockDim.x + threadIdx.x;
     if (L >= P) return;
@@ -926,10 +951,12 @@ __global__ void plan_fill(const int32_t* __restrict__ offs, const int32_t* __res
         return;
     }
     const int32_t sb = (int32_t)slot_base[L];
-    splits[split_base[L]] = SplitInfo{w, sb, ns, 0};
+    const int64_t sid = split_base[L];
+    splits[sid] = SplitInfo{w, sb, ns, 0};
     for (int32_t k = 0; k < ns; ++k) {
         const int32_t a = tb + k * seg;
         items[ib + k] = Item{w, a, min(te, a + seg), sb + k};
+        slot_split[sb + k] = (int32_t)sid;
     }
 }
 
@@ -1073,7 +1100,7 @@ static f3s_status build_plan_sets(f3s_plan* p, const int32_t* d_window_offsets,
     p->T = h[0];
     const int32_t seg_m = (int32_t)h[1], seg_d = (int32_t)h[2];
     p->has_dense = automatic && (team_d != team_m || (team_d == 1 && seg_d != seg_m));
-    int64_t max_slots = 0;
+    int64_t max_slots = 0, max_split = 0;
     for (int k = 0; k < nsets; ++k) {
         f3s_item_set& set = k == 0 ? p->masked : p->dense;
         if (k == 1 && !p->has_dense) break;
@@ -1085,9 +1112,16 @@ static f3s_status build_plan_sets(f3s_plan* p, const int32_t* d_window_offsets,
         if (set.num_slots > max_slots) max_slots = set.num_slots;
         F3S_TRY(set.items.reserve(sizeof(Item) * (size_t)(set.num_items + 1), st));
         F3S_TRY(set.splits.reserve(sizeof(SplitInfo) * (size_t)(set.num_split + 1), st));
+        F3S_TRY(set.slot_split.reserve(sizeof(int32_t) * (size_t)(set.num_slots + 1), st));
+        if (set.num_split > max_split) max_split = set.num_split;
     }
     F3S_TRY(p->partials.reserve(sizeof(float) * (size_t)kPartialFloats * H * (size_t)(max_slots + 1),
                                 st));
+    // the in-launch merge's arrival counts start at zero (each pass leaves
+    // them so); both sets share them, as they share the partials
+    const size_t cnt_b = sizeof(int32_t) * (size_t)H * (size_t)(max_split + 1);
+    F3S_TRY(p->counters.reserve(cnt_b, st));
+    F3S_HIP(hipMemsetAsync(p->counters.ptr, 0, cnt_b, st));
     for (int k = 0; k < nsets && P > 0; ++k) {
         if (k == 1 && !p->has_dense) break;
         f3s_item_set& set = k == 0 ? p->masked : p->dense;
@@ -1095,7 +1129,8 @@ static f3s_status build_plan_sets(f3s_plan* p, const int32_t* d_window_offsets,
         hipLaunchKernelGGL(plan_fill, dim3((unsigned)ceil_div(P, 256)), dim3(256), 0, st,
                            d_window_offsets, seq, W, P, set.seg, set.team, bk, bk + (P + 1),
                            bk + 2 * (size_t)(P + 1), reinterpret_cast<Item*>(set.items.ptr),
-                           reinterpret_cast<SplitInfo*>(set.splits.ptr));
+                           reinterpret_cast<SplitInfo*>(set.splits.ptr),
+                           reinterpret_cast<int32_t*>(set.slot_split.ptr));
         F3S_HIP(hipGetLastError());
     }
     // the plan is complete (and its memory usable on any stream) on return
@@ -1147,9 +1182,6 @@ static void launch_mw(const AttnParams& p, int64_t waves, hipStream_t st)
         hipLaunchKernelGGL((fused_attention_kernel<MODE, 4, WIDE, 1>),
                            dim3((unsigned)ceil_div(waves, 4)), dim3(4 * kWave), 0, st, p);
     }
-    if (p.num_split > 0)
-        hipLaunchKernelGGL(merge_partials_kernel,
-                           dim3((unsigned)ceil_div(p.num_split * p.H, 4)), dim3(256), 0, st, p);
 }
 
 template <int MODE>
@@ -1176,6 +1208,8 @@ static f3s_status launch(AttnParams p, int32_t H, float scale, hipStream_t st)
                         p.num_split == 0 && !wide_features(p.n, H),
                     "attention: invalid team launch");
     }
+    F3S_REQUIRE(p.num_split == 0 || (p.items && p.splits && p.slot_split && p.counters && p.partials),
+                "attention: split windows need the plan's merge state");
     if (!p.tile_mask)
         launch_m<kModeDense>(p, waves, st);
     else if (p.chunk_base)
@@ -1464,8 +1498,10 @@ f3s_status f3s_plan_destroy(f3s_plan* plan)
     for (f3s_item_set* set : {&plan->masked, &plan->dense}) {
         set->items.release_idle();
         set->splits.release_idle();
+        set->slot_split.release_idle();
     }
     plan->partials.release_idle();
+    plan->counters.release_idle();
     plan->chunk_base.release_idle();
     plan->columns.release_idle();
     if (switch_dev) (void)hipSetDevice(cur);
@@ -1562,6 +1598,8 @@ f3s_status f3s_attention_fwd_planned(const f3s_plan* plan, const uint16_t* Q, co
     p.xcd_contiguous = plan->xcd_contiguous;
     p.partials = reinterpret_cast<float*>(plan->partials.ptr);
     p.splits = reinterpret_cast<const SplitInfo*>(set.splits.ptr);
+    p.slot_split = reinterpret_cast<const int32_t*>(set.slot_split.ptr);
+    p.counters = reinterpret_cast<int32_t*>(plan->counters.ptr);
     p.num_split = set.num_split;
     p.team = set.team;
     if (d_tile_mask && d_tile_mask == plan->compiled_tile_mask &&

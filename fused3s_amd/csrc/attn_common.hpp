@@ -85,6 +85,9 @@ struct AttnParams {
     int32_t heavy_mode;              // order-sequence launches: 0 every entry; 1 all but the
                                      // heavy windows among the first kHeavyMaxWindows
                                      // entries; 2 only those (teams)
+    const int32_t* slot_split;       // planned launch: the split window of each partial slot
+    int32_t* counters;               // planned launch: segments arrived per (split window,
+                                     // head); zero between passes
 };
 
 // A window is heavy for the unplanned launch's teams when its tiles exceed
@@ -189,6 +192,17 @@ __device__ __forceinline__ h8 load_h8(__amdgpu_buffer_rsrc_t rs, uint32_t off)
 // non-temporal loads over the whole pass measured much slower there.
 constexpr int kStreamLoad = 2;      // the `nt` bit of a buffer load's cache policy
 constexpr int32_t kNearCols = 256;
+
+// Cache policy sc0 | sc1 (system coherence) of a buffer load or store: the
+// store writes through to memory and the load does not take a line another
+// XCD's L2 may hold stale.  The segments of a split window hand their
+// partials to the last of them this way (each XCD has its own L2), instead
+// of device-scope fences, which on gfx950 write back and invalidate the
+// whole L2 of the XCD.
+constexpr int kCoherent = 1 | 16;
+// s_waitcnt immediate (gfx9 encoding) for vmcnt(0), expcnt and lgkmcnt left
+// open: wait until every vector memory operation of the wave is done.
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 // Inclusive prefix sum over the wave with DPP row shifts and row broadcasts.
 __device__ __forceinline__ int wave_scan_incl(int x)

@@ -5,12 +5,13 @@
 #include "attn_common.hpp"
 
 // Work items of one segment size: windows with more than `seg` tiles are cut
-// into segments whose (m, l, O) partials a second launch merges.
+// into segments whose (m, l, O) partials the last segment of the window to
+// finish merges, inside the same launch.
 struct f3s_item_set {
     int32_t seg = 0;
     int32_t team = 1;   // > 1: every window is one team of this many items, merged in LDS
     int64_t num_items = 0, num_split = 0, num_slots = 0;
-    f3s::DeviceBuffer items, splits;
+    f3s::DeviceBuffer items, splits, slot_split;   // slot_split: the split of each slot
 };
 
 struct f3s_plan {
@@ -30,6 +31,9 @@ struct f3s_plan {
     // (m, l, O) partials of split-window segments, sized for the set with the
     // most slots: both sets share it, since a plan serves one pass at a time
     f3s::DeviceBuffer partials;
+    // segments arrived per (split window, head), for the in-launch merge;
+    // zero between passes (the last segment resets its window's count)
+    f3s::DeviceBuffer counters;
     // compiled column lists (f3s_plan_compile) and the structure they describe
     f3s::DeviceBuffer chunk_base, columns;
     const int32_t* compiled_block_col = nullptr;

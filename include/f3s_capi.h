@@ -213,9 +213,10 @@ f3s_status f3s_naive_attention_fwd(const float* Q, const float* K, const float* 
 
 /* Planned execution (no reference counterpart; the reference relies on the
  * window sort alone, include/utils.cuh:48-59).  A plan splits windows with
- * more than `seg_tiles` tiles into segments processed by separate waves; a
- * second, small launch merges each split window's segments in a fixed order
- * (deterministic), so hub windows do not serialise.  seg_tiles = 0 chooses
+ * more than `seg_tiles` tiles into segments processed by separate waves; the
+ * last segment of each split window to finish merges its segments in a fixed
+ * order (deterministic), inside the same launch, so hub windows do not
+ * serialise.  seg_tiles = 0 chooses
  * automatically: on small graphs (W*H <= 2048) the teams of f3s_attention_fwd
  * (same items, same bits), else segment sizes from T*H.  Windows run in d_window_order (the reference's descending
  * sort) or, when it is NULL, in natural order with consecutive windows kept
