@@ -522,6 +522,34 @@ def test_padded_buffers_with_nan_padding(gpu):
             assert np.all(got[n:].view(np.uint32) == 0xFFFFFFFF), (what, masked)
 
 
+@pytest.mark.parametrize("H", [1, 3])
+def test_plan_split_merge_state_across_passes(gpu, H):
+    # Split windows merge inside the launch: the last segment of a window to
+    # finish merges the partials and resets the window's arrival count.  One
+    # plan (both item sets share its partials and counts) serves masked and
+    # tile-dense passes in turn; every pass must give the first pass's bits
+    # on every row (a count left non-zero would leave its window's rows NaN)
+    # and meet the oracle.
+    rp, ci = star_graph(6000, hubs=(0, 5, 2999))
+    p = Problem(gpu, rp, ci, H=H, normal=True, seed=47)
+    plan = gpu.Plan(p.bsf, gpu.window_order_device(p.bsf), H=H, seg_tiles=48)
+    plan.compile()
+    assert plan.num_split > 0
+    first = {}
+    for rep in range(3):
+        for masked in (True, False, True):
+            p.dO.fill_bytes(0xFF)
+            plan.forward(p.dQ, p.dK, p.dV, p.dO, masked=masked, scale=0.125)
+            gpu.synchronize()
+            got = p.dO.numpy()
+            if masked not in first:
+                assert_close(got, p.oracle(masked, scale=0.125),
+                             f"split merge, H={H}, masked={masked}")
+                first[masked] = got
+            assert np.array_equal(got.view(np.uint32), first[masked].view(np.uint32)), \
+                (H, rep, masked)
+
+
 def test_attention_deterministic(gpu):
     rp, ci = star_graph(5000, hubs=(1,))
     p = Problem(gpu, rp, ci, normal=True, seed=4)
