@@ -54,7 +54,7 @@ CHUNK = 32
 BELOW_L2_RATE = 7.3e12
 HBM_PEAK = 8.0e12
 # the measured pass (profiles/pmc_traffic_cfg4.txt)
-MEASURED = {"below_l2_bytes": 3.937e9, "l2_read_hit_rate": 0.1995}
+MEASURED = {"below_l2_bytes": 3.950e9, "l2_read_hit_rate": 0.2023}
 PARTIAL_BYTES = 4224
 HOT_DEGREE = 64                       # selective policy: rows of at least this degree cached
 
