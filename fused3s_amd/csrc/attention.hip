@@ -852,16 +852,19 @@ static f3s_status launch_schedule(const int32_t* d_window_offsets, const int32_t
 
 // Segment sizes of an automatic plan.  A window is cut into segments only
 // when it is well above the mean window (4x masked, 2x tile-dense: cutting
-// every window of a uniform graph just adds merge traffic) and a large share
-// of one wave slot's part of the pass (5,120 slots; a tenth of it for
-// tile-dense).  seg[0] serves masked passes, seg[1] tile-dense ones.
+// every window of a uniform graph just adds merge traffic) and, masked, above
+// 1/3072 of the pass's tile-heads (tile-dense: 1/51200).  Forced masked sizes
+// on config 4 (15.9 M tiles, one head) ran flat from 3,584 to 6,144 tiles
+// (546-549 us) against 557 us at 1/8192 (1,936 tiles) and 571 us at 1,024:
+// the heaviest windows, which the descending order starts first, need few
+// segments.  seg[0] serves masked passes, seg[1] tile-dense ones.
 __host__ __device__ __forceinline__ void auto_segments(int64_t T, int32_t W, int32_t H,
                                                        int64_t seg[2])
 {
     const int64_t mean = W > 0 ? (T + W - 1) / W : 0;
     int64_t m = 256, dd = 16;
     if (4 * mean > m) m = 4 * mean;
-    if ((T * H + 8191) / 8192 > m) m = (T * H + 8191) / 8192;
+    if ((T * H + 3071) / 3072 > m) m = (T * H + 3071) / 3072;
     if (2 * mean > dd) dd = 2 * mean;
     if ((T * H + 51199) / 51200 > dd) dd = (T * H + 51199) / 51200;
     seg[0] = m < INT32_MAX ? m : INT32_MAX;

@@ -79,12 +79,12 @@ def _lib() -> C.CDLL:
 def plan_items(offs: np.ndarray, order: np.ndarray, H: int = 1):
     """The planned pass's items (window, first tile, end tile) in launch
     order: attention.hip's auto_segments (masked: max(256, 4 mean,
-    ceil(T H / 8192)) tiles) and plan_fill (a window of more than seg tiles
+    ceil(T H / 3072)) tiles) and plan_fill (a window of more than seg tiles
     becomes ceil(tiles / seg) consecutive segments)."""
     W = len(offs) - 1
     T = int(offs[-1])
     mean = -(-T // W)
-    seg = max(256, 4 * mean, -(-T * H // 8192))
+    seg = max(256, 4 * mean, -(-T * H // 3072))
     tb, te = offs[order].astype(np.int64), offs[order + 1].astype(np.int64)
     ns = np.where(te - tb > seg, -(-(te - tb) // seg), 1)
     w = np.repeat(order, ns)
