@@ -22,16 +22,19 @@
 //   * count_waves: the count pass of graphs whose bitmap is small (W <=
 //     65,536 windows): one window per wave with a bitmap of its own, no
 //     workgroup barrier;
-//   * convert_hubs: the windows with more edges (listed by convert_light),
-//     one 1024-thread workgroup each -- or, on graphs too wide for one
-//     bitmap, every window with 256 threads, the bitmap swept in column
-//     slices of kSliceCols block columns (only slices holding an edge of the
-//     window are visited).  Each thread owns a contiguous run of the
-//     window's edges and merges consecutive edges that hit the same LDS word
-//     before its atomic; windows with more than NT * kEPT edges re-read them
-//     from memory and OR their masks straight into the zeroed output;
-//   * bitmap words are cleared edge by edge after use, so no pass touches
-//     all W / 32 words per window.
+//   * the windows with more edges (hubs), which the main pass lists: when
+//     counting, count_hubs takes each with a 512-thread workgroup (any
+//     order); when filling, rank_hubs orders them heaviest first and
+//     convert_hubs gives each a 1024-thread workgroup;
+//   * convert_hubs, per window: on graphs too wide for one bitmap it takes
+//     every window with 256 threads, the bitmap swept in column slices of
+//     kSliceCols block columns (only slices holding an edge of the window
+//     are visited).  Each thread owns a contiguous run of the window's edges
+//     and merges consecutive edges that hit the same LDS word before its
+//     atomic; windows with more than NT * kEPT edges re-read them from
+//     memory and OR their masks straight into the zeroed output;
+//   * the main passes clear bitmap words edge by edge after use, so no
+//     window touches all W / 32 words.
 // The per-window work is O(E) plus a few barriers; the output is
 // deterministic and does not depend on the order of columns in a row.
 // Counts are scanned into window_offsets with the device scan of runtime.hip.
@@ -43,14 +46,14 @@
 namespace f3s {
 
 constexpr int kConvThreads = 256;                 // persistent kernel; per-window fallback
-constexpr int kHubThreads = 1024;                 // hub windows
-constexpr int kBitWords = 2048;                   // bitmap words per column slice
+constexpr int kHubThreads = 1024;                 // hub windows of the fill pass
+constexpr int kBitWords = 2048;                  // bitmap words per column slice
 constexpr int kSumWords = kBitWords / 32;         // summary: one bit per bitmap word
 constexpr int kSliceCols = kBitWords * 32;        // block columns per slice
 constexpr int kMaxSlices = 2048;                  // >= ceil(2^27 / kSliceCols)
 constexpr int kMaskTiles = 256;                   // tile masks staged in LDS at once
 constexpr int kEPT = 8;                           // edges per thread kept in registers
-constexpr int kHubBatch = 4;                      // edge loads in flight per thread, hub windows
+constexpr int kHubBatch = 4;                      // edge loads in flight per thread, wide windows
 static_assert(kSumWords == kWave, "the summary is scanned by one wave");
 
 enum ConvErr : int32_t { kErrNone = 0, kErrRowPtr = 1, kErrCol = 2, kErrCount = 4 };
@@ -66,7 +69,7 @@ struct ConvLds {
     uint32_t summary[FILL ? kSumWords : 1];    // non-empty bitmap words
     uint32_t slices[kMaxSlices / 32];          // slices holding at least one edge
     int32_t rp[17];
-    int32_t scan[kHubThreads / kWave];
+    int32_t scan[MT / kWave];
     int32_t nlist;
     int32_t bad;
 };
@@ -106,9 +109,9 @@ __device__ __forceinline__ int row_of_edge(const int32_t* rp, int nrows, int32_t
     return r;
 }
 
-// One window by one workgroup of NT threads, any edge count (the hub windows
-// the persistent kernel hands over, or every window of a graph too wide for
-// its bitmap).  Pass kind: COUNT writes counts[w]; FILL
+// One window by one workgroup of NT threads, any edge count (every window of
+// a graph too wide for the persistent kernel's bitmap).  Pass kind: COUNT
+// writes counts[w]; FILL
 // writes block_col / tile_mask at window_offsets[w] and checks the count
 // against the offsets.
 template <bool FILL, int NT>
@@ -392,9 +395,9 @@ convert_one_window(ConvLds<FILL, NT>& L, int32_t w, const int32_t* __restrict__ 
     }
 }
 
-// The hub windows listed by convert_light (hubs != NULL), or every window
-// (hubs == NULL: graphs too wide for convert_light's bitmap); a workgroup per
-// window.
+// The hub windows of the fill pass, heaviest first (hubs != NULL; listed by
+// the main pass, ordered by rank_hubs), or every window (hubs == NULL:
+// graphs too wide for convert_light's bitmap); a workgroup per window.
 template <bool FILL, int NT>
 __global__ void __launch_bounds__(NT)
 convert_hubs(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_idx,
@@ -404,14 +407,14 @@ convert_hubs(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ co
              const int32_t* __restrict__ num_hubs, int32_t* __restrict__ err)
 {
     __shared__ ConvLds<FILL, NT> L;
-    // convert_light lists each window at most once (num_hubs <= W); the clamp
+    // the main pass lists each window at most once (num_hubs <= W); the clamp
     // keeps the list read inside its W + 1 entries whatever the count holds
     const int32_t nh = hubs ? min(*num_hubs, W) : W;
     for (int32_t i = blockIdx.x; i < nh; i += gridDim.x) {
         const int32_t w = hubs ? hubs[i] : i;
         if (w < 0 || w >= W) continue;   // uniform
         convert_one_window<FILL, NT>(L, w, row_ptr, col_idx, n, nnz, W, counts, window_offsets,
-                                 block_col, tile_mask, err);
+                                     block_col, tile_mask, err);
     }
 }
 
@@ -440,13 +443,34 @@ convert_hubs(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ co
 // The per-edge work is a handful of VALU operations and one or two LDS
 // atomics: the passes are bound by instruction issue, and the fill pass also
 // by the occupancy its LDS allows, so they keep no per-edge state beyond the
-// column (and, filling, the row) and stage no more than kMaskTiles tiles.  Windows with more edges
-// are listed for convert_hubs, so that one heavy window never holds up the
-// windows queued behind it in this workgroup.
+// column (and, filling, the row) and stage no more than kMaskTiles tiles.
+// Windows with more edges are listed for the hub launches, so that one heavy
+// window never holds up the windows queued behind it in this workgroup.
 // ---------------------------------------------------------------------------
 constexpr int kLightEPT = 4;                      // edges per thread, light windows
 constexpr int kLightEdges = kConvThreads * kLightEPT;
 constexpr int kLightMaxWords = 8192;              // bitmap words: W <= 262,144 (n <= 4,194,304)
+constexpr int kHubCountThreads = 512;             // count_hubs workgroup
+
+// The hub windows (more than kLightEdges edges), listed by the main passes:
+// entry {window, first edge, edges, 0}, from the window description the
+// main pass has already validated.
+struct HubList {
+    int32_t* count;   // entries listed (atomic; zeroed before the main pass)
+    int4* hubs;       // [cap]
+    int32_t cap;      // entries `hubs` holds (each window is listed at most once)
+};
+
+// Lists window w (edges [e0, e0 + E)).  One thread lists a window: a listing
+// spread over a wave (a broadcast of the atomic's result) measured 40 %
+// slower in convert_light's fill pass, whose other waves wait for it at a
+// barrier.
+__device__ __forceinline__ void list_hub(const HubList& hl, int32_t w, int32_t e0, int32_t E)
+{
+    const int32_t i = atomicAdd(hl.count, 1);
+    if (i < hl.cap) hl.hubs[i] = make_int4(w, e0, E, 0);
+}
+
 constexpr int kMetaInts = 20;                     // rp[0..16], out_base, expect, flags
 constexpr int kMetaSlots = 3;                     // windows w_i, w_{i+1}, w_{i+2}
 constexpr int kMiscInts = 8;                      // cnt[2], total[2], bad
@@ -628,8 +652,7 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
                                              int32_t* __restrict__ counts,
                                              int32_t* __restrict__ block_col,
                                              uint16_t* __restrict__ tile_mask,
-                                             int32_t* __restrict__ hubs,
-                                             int32_t* __restrict__ num_hubs,
+                                             const HubList& hl,
                                              int32_t* __restrict__ err)
 {
     const int tid = threadIdx.x;
@@ -640,12 +663,12 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
                         (!FILL || (m.flags & kFlagOutOk));
 
     if (!usable || m.E > kLightEdges || m.E == 0) {
-        // hub (listed for convert_hubs), empty or rejected window: no tiles here
-        if (tid == 0) {
-            if (usable && m.E > 0) {
-                const int32_t i = atomicAdd(num_hubs, 1);
-                hubs[i] = w;
-            } else if (FILL) {
+        // hub (listed for count_hubs / convert_hubs, which also write its
+        // count or tiles), empty or rejected window: no tiles here
+        if (usable && m.E > 0) {
+            if (tid == 0) list_hub(hl, w, m.e0, m.E);
+        } else if (tid == 0) {
+            if (FILL) {
                 if (usable && m.expect != 0) atomicOr(err, kErrCount);
             } else {
                 counts[w] = 0;
@@ -770,8 +793,7 @@ __global__ void __launch_bounds__(kConvThreads) __attribute__((amdgpu_waves_per_
 convert_light(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_idx,
               int32_t n, int64_t nnz, int32_t W, int32_t* __restrict__ counts,
               const int32_t* __restrict__ window_offsets, int32_t* __restrict__ block_col,
-              uint16_t* __restrict__ tile_mask, int32_t* __restrict__ hubs,
-              int32_t* __restrict__ num_hubs, int32_t* __restrict__ err)
+              uint16_t* __restrict__ tile_mask, HubList hl, int32_t* __restrict__ err)
 {
     const LightLayout lay = light_layout(W, FILL);
     const LightLds L = light_lds(lay);
@@ -825,7 +847,7 @@ convert_light(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ c
             aheadY = fetch_meta<FILL>(w + 3 * G, W, n, row_ptr, window_offsets);
             issue_edges<FILL>(L, s1, col_idx, colB, rowsB, cntB);
             light_window<FILL>(L, slot, w, colA, rowsA, cntA, round, n, counts, block_col,
-                               tile_mask, hubs, num_hubs, err);
+                               tile_mask, hl, err);
             w += G;
             slot = s1;
             if (w >= W) break;
@@ -837,7 +859,7 @@ convert_light(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ c
             aheadX = fetch_meta<FILL>(w + 3 * G, W, n, row_ptr, window_offsets);
             issue_edges<FILL>(L, s1, col_idx, colA, rowsA, cntA);
             light_window<FILL>(L, slot, w, colB, rowsB, cntB, round, n, counts, block_col,
-                               tile_mask, hubs, num_hubs, err);
+                               tile_mask, hl, err);
             w += G;
             slot = s1;
             if (w >= W) break;
@@ -856,7 +878,7 @@ convert_light(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ c
 // k keeps the count of the batch's k-th window): gfx950 counts loads and
 // stores with one counter, so a store pending at every window would make
 // each wait a wait for the prefetched loads too.  Windows of more than
-// kLightEdges edges are listed for convert_hubs, which writes their counts
+// kLightEdges edges are listed for count_hubs, which writes their counts
 // (the zero this pass leaves there is overwritten).  Same counts, same hub
 // list and same error bits as convert_light<false>; on graphs of many block
 // columns the bitmap per wave leaves fewer windows in flight per CU than
@@ -923,8 +945,8 @@ __device__ __forceinline__ void wave_issue_cols(const WaveWin& d,
 
 __global__ void __launch_bounds__(kWaveCountWaves * kWave)
 count_waves(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_idx, int32_t n,
-            int64_t nnz, int32_t W, int32_t* __restrict__ counts, int32_t* __restrict__ hubs,
-            int32_t* __restrict__ num_hubs, int32_t* __restrict__ err)
+            int64_t nnz, int32_t W, int32_t* __restrict__ counts, HubList hl,
+            int32_t* __restrict__ err)
 {
     const int words = (W + 31) / 32;
     const int lane = threadIdx.x & (kWave - 1);
@@ -947,7 +969,7 @@ count_waves(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col
         if (!d.ok) {
             if (lane == 0) atomicOr(err, kErrRowPtr);
         } else if (d.E > kLightEdges) {
-            if (lane == 0) hubs[atomicAdd(num_hubs, 1)] = (int32_t)wn;
+            if (lane == 0) list_hub(hl, (int32_t)wn, d.e0, d.E);
         } else if (d.E > 0) {
             int fresh = 0;
 #pragma unroll
@@ -1006,48 +1028,105 @@ count_waves(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col
     if (__any(bad) && lane == 0) atomicOr(err, kErrCol);
 }
 
-// Hub windows heaviest first.  convert_light lists them in the order its
-// workgroups find them; rank_hubs writes the list again, ordered by
-// descending edge count (ties: ascending window index, so the order is
-// deterministic), and the hub launch that follows gives each listed window a
-// workgroup of its own, dispatched in list order, so the longest windows
-// start first.  Every workgroup of rank_hubs loads the keys of the whole list
-// (up to kHubSortCap) into LDS and places 64 of them at their ranks, four
-// lanes per entry each counting the smaller keys in a quarter of the list;
-// keys are unique, so the ranks are a permutation.  A longer list is copied
-// as listed.
+// ---------------------------------------------------------------------------
+// count_hubs: the count pass of the hub windows the main pass listed, one
+// kHubCountThreads workgroup per window (any order, a grid-stride loop over
+// the list): every edge ORs its block column's bit into an LDS bitmap, and
+// the bits set for the first time add up to the window's tile count.  The
+// edges are read in coalesced chunks of kHubCountThreads * kHubCountEPT, all
+// loads of a chunk in flight at once.  Measured on config 4's 1,310 hubs:
+// 13 us, against 29 us with the fill pass's 1024-thread kernel plus 10 us to
+// order the list first.
+// ---------------------------------------------------------------------------
+constexpr int kHubCountEPT = 8;
+
+__global__ void __launch_bounds__(kHubCountThreads)
+count_hubs(const int32_t* __restrict__ col_idx, int32_t n, int64_t nnz, int32_t W,
+           int32_t* __restrict__ counts, HubList hl, int32_t* __restrict__ err)
+{
+    constexpr int NT = kHubCountThreads;
+    constexpr int32_t kChunk = NT * kHubCountEPT;
+    uint32_t* bits = reinterpret_cast<uint32_t*>(conv_lds);
+    const int words4 = ((W + 31) / 32 + 3) & ~3;
+    int32_t* scan = reinterpret_cast<int32_t*>(conv_lds) + words4;   // [NT / 64]
+    int32_t* bad = scan + NT / kWave;
+    const int tid = threadIdx.x;
+    const int32_t nh = min(*hl.count, hl.cap);
+    if ((int32_t)blockIdx.x >= nh) return;   // uniform
+    for (int g = tid; g < words4 / 4; g += NT)
+        reinterpret_cast<uint4*>(bits)[g] = make_uint4(0u, 0u, 0u, 0u);
+    if (tid == 0) *bad = 0;
+    for (int32_t i = blockIdx.x; i < nh; i += gridDim.x) {
+        const int4 h = hl.hubs[i];
+        const int32_t w = h.x, e0 = h.y, E = h.z;
+        // (the main pass listed the window with usable row pointers; the
+        // check keeps every access in bounds whatever the list holds)
+        if ((uint32_t)w >= (uint32_t)W || e0 < 0 || E <= 0 || (int64_t)e0 + E > nnz)
+            continue;   // uniform
+        __syncthreads();   // the previous window's bitmap is clear
+        int32_t fresh = 0;
+        for (int64_t c0 = 0; c0 < E; c0 += kChunk) {
+            int32_t col[kHubCountEPT];
+#pragma unroll
+            for (int j = 0; j < kHubCountEPT; ++j) {
+                const int64_t e = c0 + tid + NT * j;
+                col[j] = e < E ? col_idx[e0 + e] : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < kHubCountEPT; ++j) {
+                const int64_t e = c0 + tid + NT * j;
+                if (e >= E) continue;
+                const int32_t c = col[j];
+                if (c < 0 || c >= n) {
+                    *bad = 1;
+                    continue;
+                }
+                const uint32_t bit = 1u << ((c >> 4) & 31);
+                fresh += (atomicOr(&bits[c >> 9], bit) & bit) == 0u;
+            }
+        }
+        int32_t T;
+        (void)block_exclusive_scan<NT>(fresh, scan, T);   // barriers inside: the marks are done
+        if (tid == 0) counts[w] = T;
+        for (int g = tid; g < words4 / 4; g += NT)
+            reinterpret_cast<uint4*>(bits)[g] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
+    if (tid == 0 && *bad) atomicOr(err, kErrCol);
+}
+
+// Hub windows heaviest first, for the fill pass.  The main pass lists them
+// in the order its workgroups find them; rank_hubs writes their windows again,
+// ordered by descending edge count (ties: ascending window index, so the
+// order is deterministic), and the hub launch that follows gives each listed
+// window a workgroup of its own, dispatched in list order, so the longest
+// windows start first.  Every workgroup of rank_hubs loads the keys of the
+// whole list (up to kHubSortCap) into LDS and places 64 of them at their
+// ranks, four lanes per entry each counting the smaller keys in a quarter of
+// the list; keys are unique, so the ranks are a permutation.  A longer list
+// is copied as listed.
 constexpr int kHubSortCap = 4096;
 constexpr int kHubLaunch = 2048;   // hub-launch workgroups (one per listed window up to this)
 
 __global__ void __launch_bounds__(256)
-rank_hubs(const int32_t* __restrict__ row_ptr, int32_t n, int32_t W,
-          const int32_t* __restrict__ hubs, const int32_t* __restrict__ num_hubs,
-          int32_t* __restrict__ sorted)
+rank_hubs(int32_t W, HubList hl, int32_t* __restrict__ sorted)
 {
     __shared__ __align__(16) uint64_t key[kHubSortCap];
-    const int32_t nh = min(*num_hubs, W);
+    const int32_t nh = min(*hl.count, hl.cap);
     const int tid = threadIdx.x;
     if (nh > kHubSortCap) {   // uniform: copy in listing order
         for (int64_t i = (int64_t)blockIdx.x * 256 + tid; i < nh; i += (int64_t)gridDim.x * 256)
-            sorted[i] = hubs[i];
+            sorted[i] = hl.hubs[i].x;
         return;
     }
     const int32_t base = blockIdx.x * 64;
     if (base >= nh) return;   // uniform
-    // The thread's list entries, then their row pointers: two rounds of loads
-    // in flight instead of one dependent pair per entry.
     constexpr int kPer = kHubSortCap / 256;
-    int32_t wv[kPer], lo[kPer], hi[kPer];
+    int4 h[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const int i = tid + 256 * k;
-        wv[k] = i < nh ? hubs[i] : -1;
-    }
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const bool ok = (uint32_t)wv[k] < (uint32_t)W;
-        lo[k] = ok ? row_ptr[wv[k] * 16] : 0;
-        hi[k] = ok ? row_ptr[min(n, wv[k] * 16 + 16)] : 0;
+        h[k] = i < nh ? hl.hubs[i] : make_int4(-1, 0, 0, 0);
     }
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -1056,9 +1135,9 @@ rank_hubs(const int32_t* __restrict__ row_ptr, int32_t n, int32_t W,
         const int i = tid + 256 * k;
         if (i >= nh) break;
         uint64_t key_i = (0xffffffffull << 32) | (uint32_t)i;
-        if ((uint32_t)wv[k] < (uint32_t)W) {
-            const uint32_t edges = (uint32_t)min(max(1, hi[k] - lo[k]), 0x7fffffff);
-            key_i = ((uint64_t)(~edges) << 32) | (uint32_t)wv[k];
+        if ((uint32_t)h[k].x < (uint32_t)W) {
+            const uint32_t edges = (uint32_t)max(1, h[k].z);
+            key_i = ((uint64_t)(~edges) << 32) | (uint32_t)h[k].x;
         }
         key[i] = key_i;
     }
@@ -1110,15 +1189,14 @@ __global__ void fill_status(const int32_t* __restrict__ window_offsets, int32_t 
 }
 
 // Per-call workspace of the converter, one allocation: status words (error
-// bits, hub count, two int64 results), the hub window list as found and as
+// bits, the hub count, two int64 results), the hub list as found and (fill)
 // ordered heaviest first and, for the count pass, the counts, their int64
 // scan and its temporaries.
 struct ConvertScratch {
     int32_t* err;
-    int32_t* num_hubs;
-    int64_t* status;
-    int32_t* hubs;
+    HubList hl;
     int32_t* hubs_sorted;
+    int64_t* status;
     int32_t* counts;
     int64_t* offs64;
     int64_t* tmp;
@@ -1126,22 +1204,24 @@ struct ConvertScratch {
 
 static f3s_status convert_scratch(StreamBuffer& buf, int32_t W, bool count, ConvertScratch& s)
 {
-    const size_t head = 32;   // err, num_hubs, pad, status[2]
-    const size_t hubs = sizeof(int32_t) * ((size_t)W + 1);
+    const size_t head = 32;   // err, hub count, pad, status[2]
+    const size_t hubs = sizeof(int4) * ((size_t)W + 1);
+    const size_t sorted = count ? 0 : sizeof(int32_t) * ((size_t)W + 1);
     const size_t counts = count ? sizeof(int32_t) * (size_t)W : 0;
     const size_t offs = count ? sizeof(int64_t) * ((size_t)W + 1) : 0;
     const size_t tmp = count ? sizeof(int64_t) * (size_t)scan_tmp_elems(W) : 0;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    F3S_TRY(buf.reserve(al(head) + 2 * al(hubs) + al(counts) + al(offs) + al(tmp)));
+    F3S_TRY(buf.reserve(al(head) + al(hubs) + al(sorted) + al(counts) + al(offs) + al(tmp)));
     char* p = static_cast<char*>(buf.ptr);
     s.err = reinterpret_cast<int32_t*>(p);
-    s.num_hubs = s.err + 1;
+    s.hl.count = s.err + 1;
     s.status = reinterpret_cast<int64_t*>(p + 16);
     p += al(head);
-    s.hubs = reinterpret_cast<int32_t*>(p);
+    s.hl.hubs = reinterpret_cast<int4*>(p);
+    s.hl.cap = W + 1;
     p += al(hubs);
     s.hubs_sorted = reinterpret_cast<int32_t*>(p);
-    p += al(hubs);
+    p += al(sorted);
     s.counts = reinterpret_cast<int32_t*>(p);
     p += al(counts);
     s.offs64 = reinterpret_cast<int64_t*>(p);
@@ -1152,15 +1232,15 @@ static f3s_status convert_scratch(StreamBuffer& buf, int32_t W, bool count, Conv
 
 // One pass (count or fill) over all windows: the persistent kernel with as
 // many workgroups as fit on the device at once, then the hub windows it
-// listed (the hub launch cannot know the hub count, so it loops over the
-// list with a fixed grid).  Graphs too wide for one LDS bitmap run every
-// window through the per-window kernel.
+// listed (the hub count is known only on the device, so the hub launches
+// have a fixed grid that walks the list).  Graphs too wide for one LDS
+// bitmap run every window through the per-window kernel.
 template <bool FILL>
 static f3s_status launch_pass(const int32_t* row_ptr, const int32_t* col_idx, int32_t n,
                               int64_t nnz, int32_t W, int32_t* counts,
                               const int32_t* window_offsets, int32_t* block_col,
-                              uint16_t* tile_mask, int32_t* hubs, int32_t* hubs_sorted,
-                              int32_t* num_hubs, int32_t* err, hipStream_t stream)
+                              uint16_t* tile_mask, const HubList& hl, int32_t* hubs_sorted,
+                              int32_t* err, hipStream_t stream)
 {
     if (W <= 0) return F3S_OK;
     if ((int64_t)W > 32LL * kLightMaxWords) {
@@ -1173,34 +1253,44 @@ static f3s_status launch_pass(const int32_t* row_ptr, const int32_t* col_idx, in
     int dev = 0, cus = 0, per_cu = 0;
     F3S_HIP(hipGetDevice(&dev));
     F3S_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    if (cus < 1) cus = 1;
     if (!FILL && (int64_t)W <= 32LL * kWaveCountMaxWords) {
         // small bitmap: the count pass with one window per wave
         const uint32_t lds = (uint32_t)(sizeof(uint32_t) * kWaveCountWaves * ((W + 31) / 32));
         F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, count_waves,
                                                              kWaveCountWaves * kWave, lds));
-        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * cus;
         const int64_t need = ceil_div(W, kWaveCountWaves);
         hipLaunchKernelGGL(count_waves, dim3((unsigned)(need < resident ? need : resident)),
                            dim3(kWaveCountWaves * kWave), lds, stream, row_ptr, col_idx, n, nnz,
-                           W, counts, hubs, num_hubs, err);
+                           W, counts, hl, err);
     } else {
         const LightLayout lay = light_layout(W, FILL);
         F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, convert_light<FILL>,
                                                              kConvThreads, lay.bytes));
-        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * cus;
         const unsigned grid = (unsigned)(W < resident ? W : resident);
         hipLaunchKernelGGL((convert_light<FILL>), dim3(grid), dim3(kConvThreads), lay.bytes,
                            stream, row_ptr, col_idx, n, nnz, W, counts, window_offsets, block_col,
-                           tile_mask, hubs, num_hubs, err);
+                           tile_mask, hl, err);
     }
     F3S_HIP(hipGetLastError());
-    const int32_t rank_wgs = (int32_t)ceil_div(W < kHubSortCap ? W : kHubSortCap, 64);
-    hipLaunchKernelGGL(rank_hubs, dim3((unsigned)rank_wgs), dim3(256), 0, stream, row_ptr, n, W,
-                       hubs, num_hubs, hubs_sorted);
-    const int64_t hub_grid = kHubLaunch;
-    hipLaunchKernelGGL((convert_hubs<FILL, kHubThreads>), dim3((unsigned)(W < hub_grid ? W : hub_grid)),
-                       dim3(kHubThreads), 0, stream, row_ptr, col_idx, n, nnz, W, counts,
-                       window_offsets, block_col, tile_mask, hubs_sorted, num_hubs, err);
+    if (!FILL) {
+        const uint32_t lds = (uint32_t)(4 * ((((W + 31) / 32 + 3) & ~3) + kHubCountThreads / kWave + 4));
+        F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, count_hubs,
+                                                             kHubCountThreads, lds));
+        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * cus;
+        hipLaunchKernelGGL(count_hubs, dim3((unsigned)(W < resident ? W : resident)),
+                           dim3(kHubCountThreads), lds, stream, col_idx, n, nnz, W, counts, hl, err);
+    } else {
+        const int32_t rank_wgs = (int32_t)ceil_div(W < kHubSortCap ? W : kHubSortCap, 64);
+        hipLaunchKernelGGL(rank_hubs, dim3((unsigned)rank_wgs), dim3(256), 0, stream, W, hl,
+                           hubs_sorted);
+        hipLaunchKernelGGL((convert_hubs<true, kHubThreads>),
+                           dim3((unsigned)(W < kHubLaunch ? W : kHubLaunch)), dim3(kHubThreads), 0,
+                           stream, row_ptr, col_idx, n, nnz, W, counts, window_offsets, block_col,
+                           tile_mask, hubs_sorted, hl.count, err);
+    }
     F3S_HIP(hipGetLastError());
     return F3S_OK;
 }
@@ -1217,17 +1307,16 @@ static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, i
     StreamBuffer buf(stream);
     ConvertScratch s;
     F3S_TRY(convert_scratch(buf, W, count, s));
-    F3S_HIP(hipMemsetAsync(s.err, 0, 2 * sizeof(int32_t), stream));
+    F3S_HIP(hipMemsetAsync(s.err, 0, 2 * sizeof(int32_t), stream));   // err, hub count
     if (count) {
         F3S_TRY(launch_pass<false>(row_ptr, col_idx, n, nnz, W, s.counts, nullptr, nullptr,
-                                   nullptr, s.hubs, s.hubs_sorted, s.num_hubs, s.err, stream));
+                                   nullptr, s.hl, nullptr, s.err, stream));
         F3S_TRY(exclusive_scan_i32_to_i64(s.counts, s.offs64, W, s.tmp, stream));
         hipLaunchKernelGGL(offsets_to_i32, dim3((unsigned)ceil_div(W + 1, 256)), dim3(256), 0,
                            stream, s.offs64, window_offsets, (int64_t)W + 1, s.err, s.status);
     } else {
         F3S_TRY(launch_pass<true>(row_ptr, col_idx, n, nnz, W, nullptr, window_offsets,
-                                  block_col, tile_mask, s.hubs, s.hubs_sorted, s.num_hubs, s.err,
-                                  stream));
+                                  block_col, tile_mask, s.hl, s.hubs_sorted, s.err, stream));
         hipLaunchKernelGGL(fill_status, dim3(1), dim3(64), 0, stream, window_offsets, W, s.err,
                            s.status);
     }
