@@ -163,14 +163,30 @@ def convert_phases_ms(csr, bsf, stream) -> float:
 def time_passes(f3s, one_pass, stream, reps: int) -> np.ndarray:
     """Per-pass milliseconds from HIP events on the launch stream, after one
     untimed pass."""
+    return time_passes_cold(f3s, one_pass, stream, reps)[0]
+
+
+def time_passes_cold(f3s, one_pass, stream, reps: int):
+    """(per-pass milliseconds of `reps` passes, milliseconds of the first
+    pass before them), all from HIP events on the launch stream."""
+    c0, c1 = f3s.Event(), f3s.Event()
+    c0.record(stream)
     one_pass()
+    c1.record(stream)
     evs = [(f3s.Event(), f3s.Event()) for _ in range(reps)]
     for a, b in evs:
         a.record(stream)
         one_pass()
         b.record(stream)
     stream.synchronize()
-    return np.array([a.elapsed_ms(b) for a, b in evs])
+    return np.array([a.elapsed_ms(b) for a, b in evs]), c0.elapsed_ms(c1)
+
+
+def pass_times(t: np.ndarray, cold_ms: float) -> dict:
+    """The per-pass statistics every timed leg reports (microseconds)."""
+    return {"kernel_us": float(t.mean()) * 1e3, "kernel_us_median": float(np.median(t)) * 1e3,
+            "kernel_us_min": float(t.min()) * 1e3, "cold_first_launch_us": cold_ms * 1e3,
+            "passes": int(len(t))}
 
 
 def gather_ceiling(f3s, dK, dV, rows: int, H: int, count: int, stream, reps: int = 10,
@@ -392,7 +408,7 @@ def reference_single_thread(rp, ci, Q, K, V, n: int, d: int, min_s: float = 0.5)
 
 
 def config_legs(f3s, orc, cfgnum: int, stream, reps_masked: int = 20,
-                reps_dense: int = 5) -> dict:
+                reps_dense: int = 20) -> dict:
     """One configuration end to end on the GPU, then checked on the host:
     converter (GPU time of its two phases; output bit-exact against the
     oracle converter), the planned masked and tile-dense passes and the
@@ -437,7 +453,7 @@ def config_legs(f3s, orc, cfgnum: int, stream, reps_masked: int = 20,
     legs, outs = {}, {}
     for name, fn, sem, lnch, reps in runs:
         dO.fill_bytes(0xFF, stream)   # NaN: a row the pass does not write cannot match
-        t = time_passes(f3s, fn, stream, reps)
+        t, cold = time_passes_cold(f3s, fn, stream, reps)
         mean = float(t.mean())
         b = compulsory_bytes(n, H, bsf.W, bsf.T, kv_rows[sem], sem, lnch, ps)
         chunks = (ps["num_chunks"] if (sem and lnch == "plan") else
@@ -445,8 +461,7 @@ def config_legs(f3s, orc, cfgnum: int, stream, reps_masked: int = 20,
         issued = chunks * H * 8 * (2 * 16 * 16 * 32)
         tile_model = bsf.T * 4 * 16 * 16 * d * H
         legs[name] = {"semantics": "masked" if sem else "tile_dense", "launch": lnch,
-                      "kernel_us": mean * 1e3, "kernel_us_min": float(t.min()) * 1e3,
-                      "passes": reps, "edges_per_s": nnz / (mean * 1e-3),
+                      **pass_times(t, cold), "edges_per_s": nnz / (mean * 1e-3),
                       "compulsory_bytes": b,
                       "roofline_frac": b / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS,
                       "mfma_issued_frac": issued / (mean * 1e-3) / (MFMA_F16_PEAK_TFLOPS * 1e12),
@@ -464,6 +479,24 @@ def config_legs(f3s, orc, cfgnum: int, stream, reps_masked: int = 20,
            "attended_tile_columns": occ_sum, "mask_bits": mask_bits,
            "converter_us": conv_ms * 1e3}
     res["converter_check"] = converter_exact(orc, bsf, n, rp, ci)
+    # measured traffic below the L2, where a committed rocprofv3 profile of
+    # this configuration's planned masked pass exists (config 5; the small
+    # graphs fit in the L2 and are not profiled), with its provenance
+    prof = ROOT / "profiles" / f"pmc_traffic_cfg{cfgnum}.txt"
+    below = read_profile(prof, "bytes_per_launch") if cfgnum != 4 else None
+    if below and "masked_planned" in legs:
+        mean_ms = legs["masked_planned"]["kernel_us"] * 1e-3
+        digest = read_profile_field(prof, "sources_fused_attention")
+        legs["masked_planned"]["below_l2"] = {
+            "bytes_per_launch": below, "GBps": below / (mean_ms * 1e-3) / 1e9,
+            "frac_of_hbm_peak": below / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "l2_read_hit_rate": read_profile(prof, "l2_read_hit_rate"),
+            "profiled_kernel_avg_us": read_profile(prof, "kernel_avg_us"),
+            "kind": "HBM + Infinity Cache (rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, "
+                    "copy-calibrated)",
+            "source": str(prof.relative_to(ROOT)),
+            "commit": read_profile_field(prof, "commit"),
+            "sources_current": digest == source_digest("fused_attention")}
     offs = bsf.window_offsets.numpy()
     bcol = bsf.block_col.numpy()
     del bsf
@@ -840,18 +873,18 @@ def main() -> int:
         ref_plan = plan if plan is not None else make_plan()
         rps = ref_plan.stats()
         reps_m = max(3, min(20, args.steps))
-        reps_d = max(3, min(5, args.steps))
+        reps_d = max(3, min(20, args.steps))
 
         def leg(name, fn, sem_masked, lnch, reps):
             dO.fill_bytes(0xFF, stream)   # NaN: a row the pass does not write cannot match
-            t = time_passes(f3s, fn, stream, reps)
+            t, cold = time_passes_cold(f3s, fn, stream, reps)
             mean = float(t.mean())
             leg_outs[name] = dO.numpy(stream)
             b = compulsory_bytes(n, H, bsf.W, bsf.T, kv_rows[sem_masked], sem_masked, lnch, rps)
             rows = 2 * H * (occ_masked if sem_masked else bsf.T * 16)
             legs[name] = {"semantics": "masked" if sem_masked else "tile_dense",
-                          "kernel_us": mean * 1e3, "edges_per_s": nnz / (mean * 1e-3),
-                          "passes": reps, "compulsory_bytes": b,
+                          **pass_times(t, cold), "edges_per_s": nnz / (mean * 1e-3),
+                          "compulsory_bytes": b,
                           "roofline_frac": b / (mean * 1e-3) / 1e9 / HBM_PEAK_GBS,
                           "gathered_rows_per_s": rows / (mean * 1e-3),
                           "over_gather_ceiling": rows / (mean * 1e-3) / ceiling(sem_masked)}

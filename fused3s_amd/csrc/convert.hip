@@ -40,6 +40,8 @@
 // Counts are scanned into window_offsets with the device scan of runtime.hip.
 #include <stdio.h>
 
+#include <mutex>
+
 #include "f3s_common.hpp"
 #include "f3s_device.hpp"
 
@@ -1166,18 +1168,6 @@ rank_hubs(int32_t W, HubList hl, int32_t* __restrict__ sorted)
 
 // int64 window offsets -> the caller's int32 offsets; thread 0 also reports
 // the error bits and the tile count for the host (status[0], status[1]).
-__global__ void offsets_to_i32(const int64_t* __restrict__ in, int32_t* __restrict__ out,
-                               int64_t count, const int32_t* __restrict__ err,
-                               int64_t* __restrict__ status)
-{
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < count) out[i] = (int32_t)in[i];
-    if (i == 0) {
-        status[0] = *err;
-        status[1] = in[count - 1];
-    }
-}
-
 // The fill pass's error bits and the tile count it was given (status[0..1]).
 __global__ void fill_status(const int32_t* __restrict__ window_offsets, int32_t W,
                             const int32_t* __restrict__ err, int64_t* __restrict__ status)
@@ -1198,7 +1188,6 @@ struct ConvertScratch {
     int32_t* hubs_sorted;
     int64_t* status;
     int32_t* counts;
-    int64_t* offs64;
     int64_t* tmp;
 };
 
@@ -1208,10 +1197,9 @@ static f3s_status convert_scratch(StreamBuffer& buf, int32_t W, bool count, Conv
     const size_t hubs = sizeof(int4) * ((size_t)W + 1);
     const size_t sorted = count ? 0 : sizeof(int32_t) * ((size_t)W + 1);
     const size_t counts = count ? sizeof(int32_t) * (size_t)W : 0;
-    const size_t offs = count ? sizeof(int64_t) * ((size_t)W + 1) : 0;
     const size_t tmp = count ? sizeof(int64_t) * (size_t)scan_tmp_elems(W) : 0;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    F3S_TRY(buf.reserve(al(head) + al(hubs) + al(sorted) + al(counts) + al(offs) + al(tmp)));
+    F3S_TRY(buf.reserve(al(head) + al(hubs) + al(sorted) + al(counts) + al(tmp)));
     char* p = static_cast<char*>(buf.ptr);
     s.err = reinterpret_cast<int32_t*>(p);
     s.hl.count = s.err + 1;
@@ -1224,9 +1212,50 @@ static f3s_status convert_scratch(StreamBuffer& buf, int32_t W, bool count, Conv
     p += al(sorted);
     s.counts = reinterpret_cast<int32_t*>(p);
     p += al(counts);
-    s.offs64 = reinterpret_cast<int64_t*>(p);
-    p += al(offs);
     s.tmp = reinterpret_cast<int64_t*>(p);
+    return F3S_OK;
+}
+
+// Workgroups of `fn` (`threads` wide, `lds` bytes of dynamic LDS) resident
+// on the current device at once: the grid of a persistent pass.  Cached per
+// device, kernel and LDS size -- a conversion asks for three of them, and
+// the runtime's occupancy query is host time on every call.
+static f3s_status resident_workgroups(const void* fn, int threads, uint32_t lds, int64_t* out)
+{
+    struct Entry {
+        int dev;
+        const void* fn;
+        int threads;
+        uint32_t lds;
+        int64_t resident;
+    };
+    constexpr int kEntries = 32;
+    static std::mutex mu;
+    static Entry cache[kEntries];
+    static int used = 0, next = 0;
+    int dev = 0;
+    F3S_HIP(hipGetDevice(&dev));
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (int i = 0; i < used; ++i) {
+            const Entry& e = cache[i];
+            if (e.dev == dev && e.fn == fn && e.threads == threads && e.lds == lds) {
+                *out = e.resident;
+                return F3S_OK;
+            }
+        }
+    }
+    int cus = 0, per_cu = 0;
+    F3S_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds));
+    const int64_t r = (int64_t)(per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        cache[next] = Entry{dev, fn, threads, lds, r};
+        next = (next + 1) % kEntries;
+        if (used < kEntries) ++used;
+    }
+    *out = r;
     return F3S_OK;
 }
 
@@ -1250,25 +1279,20 @@ static f3s_status launch_pass(const int32_t* row_ptr, const int32_t* col_idx, in
         F3S_HIP(hipGetLastError());
         return F3S_OK;
     }
-    int dev = 0, cus = 0, per_cu = 0;
-    F3S_HIP(hipGetDevice(&dev));
-    F3S_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    if (cus < 1) cus = 1;
+    int64_t resident = 0;
     if (!FILL && (int64_t)W <= 32LL * kWaveCountMaxWords) {
         // small bitmap: the count pass with one window per wave
         const uint32_t lds = (uint32_t)(sizeof(uint32_t) * kWaveCountWaves * ((W + 31) / 32));
-        F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, count_waves,
-                                                             kWaveCountWaves * kWave, lds));
-        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * cus;
+        F3S_TRY(resident_workgroups(reinterpret_cast<const void*>(count_waves),
+                                    kWaveCountWaves * kWave, lds, &resident));
         const int64_t need = ceil_div(W, kWaveCountWaves);
         hipLaunchKernelGGL(count_waves, dim3((unsigned)(need < resident ? need : resident)),
                            dim3(kWaveCountWaves * kWave), lds, stream, row_ptr, col_idx, n, nnz,
                            W, counts, hl, err);
     } else {
         const LightLayout lay = light_layout(W, FILL);
-        F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, convert_light<FILL>,
-                                                             kConvThreads, lay.bytes));
-        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * cus;
+        F3S_TRY(resident_workgroups(reinterpret_cast<const void*>(convert_light<FILL>),
+                                    kConvThreads, lay.bytes, &resident));
         const unsigned grid = (unsigned)(W < resident ? W : resident);
         hipLaunchKernelGGL((convert_light<FILL>), dim3(grid), dim3(kConvThreads), lay.bytes,
                            stream, row_ptr, col_idx, n, nnz, W, counts, window_offsets, block_col,
@@ -1277,9 +1301,8 @@ static f3s_status launch_pass(const int32_t* row_ptr, const int32_t* col_idx, in
     F3S_HIP(hipGetLastError());
     if (!FILL) {
         const uint32_t lds = (uint32_t)(4 * ((((W + 31) / 32 + 3) & ~3) + kHubCountThreads / kWave + 4));
-        F3S_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, count_hubs,
-                                                             kHubCountThreads, lds));
-        const int64_t resident = (int64_t)(per_cu > 0 ? per_cu : 1) * cus;
+        F3S_TRY(resident_workgroups(reinterpret_cast<const void*>(count_hubs), kHubCountThreads,
+                                    lds, &resident));
         hipLaunchKernelGGL(count_hubs, dim3((unsigned)(W < resident ? W : resident)),
                            dim3(kHubCountThreads), lds, stream, col_idx, n, nnz, W, counts, hl, err);
     } else {
@@ -1311,9 +1334,9 @@ static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, i
     if (count) {
         F3S_TRY(launch_pass<false>(row_ptr, col_idx, n, nnz, W, s.counts, nullptr, nullptr,
                                    nullptr, s.hl, nullptr, s.err, stream));
-        F3S_TRY(exclusive_scan_i32_to_i64(s.counts, s.offs64, W, s.tmp, stream));
-        hipLaunchKernelGGL(offsets_to_i32, dim3((unsigned)ceil_div(W + 1, 256)), dim3(256), 0,
-                           stream, s.offs64, window_offsets, (int64_t)W + 1, s.err, s.status);
+        // T <= nnz <= INT32_MAX (a tile holds at least one edge): int32 offsets
+        F3S_TRY(exclusive_scan_i32_to_i32(s.counts, window_offsets, W, s.tmp, s.err, s.status,
+                                          stream));
     } else {
         F3S_TRY(launch_pass<true>(row_ptr, col_idx, n, nnz, W, nullptr, window_offsets,
                                   block_col, tile_mask, s.hl, s.hubs_sorted, s.err, stream));
