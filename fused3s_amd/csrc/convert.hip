@@ -37,7 +37,7 @@
 //     window touches all W / 32 words.
 // The per-window work is O(E) plus a few barriers; the output is
 // deterministic and does not depend on the order of columns in a row.
-// Counts are scanned into window_offsets with the device scan of runtime.hip.
+// Counts become window_offsets through counts_to_offsets (two launches).
 #include <stdio.h>
 
 #include <mutex>
@@ -1168,6 +1168,104 @@ rank_hubs(int32_t W, HubList hl, int32_t* __restrict__ sorted)
 
 // int64 window offsets -> the caller's int32 offsets; thread 0 also reports
 // the error bits and the tile count for the host (status[0], status[1]).
+// ---------------------------------------------------------------------------
+// Counts -> window_offsets in two launches: block sums, then each workgroup
+// adds up the sums of the blocks before its own (at most kOffsFusedBlocks of
+// them; wider graphs scan the sums in one workgroup first), scans its block
+// straight into the int32 offsets -- T <= nnz <= INT32_MAX, since a tile
+// holds at least one edge -- and its last workgroup writes offsets[W] and the
+// host's status words (error bits, T).
+// ---------------------------------------------------------------------------
+constexpr int kOffsThreads = 256;
+constexpr int kOffsPerThread = 8;
+constexpr int kOffsTile = kOffsThreads * kOffsPerThread;
+constexpr int64_t kOffsFusedBlocks = 1024;
+
+__global__ void __launch_bounds__(kOffsThreads)
+offsets_block_sums(const int32_t* __restrict__ counts, int64_t W, int64_t* __restrict__ sums)
+{
+    __shared__ int64_t lds[kOffsThreads / kWave];
+    const int64_t base = (int64_t)blockIdx.x * kOffsTile + (int64_t)threadIdx.x * kOffsPerThread;
+    int64_t s = 0;
+#pragma unroll
+    for (int i = 0; i < kOffsPerThread; ++i)
+        if (base + i < W) s += counts[base + i];
+    int64_t total;
+    (void)block_exclusive_scan<kOffsThreads>(s, lds, total);
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+// One workgroup: the block sums into exclusive prefix sums, in place.
+__global__ void __launch_bounds__(kOffsThreads)
+offsets_scan_sums(int64_t* __restrict__ sums, int64_t nblocks)
+{
+    __shared__ int64_t lds[kOffsThreads / kWave];
+    int64_t carry = 0;
+    for (int64_t b0 = 0; b0 < nblocks; b0 += kOffsThreads) {
+        const int64_t i = b0 + threadIdx.x;
+        const int64_t v = i < nblocks ? sums[i] : 0;
+        int64_t total;
+        const int64_t ex = block_exclusive_scan<kOffsThreads>(v, lds, total);
+        if (i < nblocks) sums[i] = carry + ex;
+        carry += total;
+    }
+}
+
+__global__ void __launch_bounds__(kOffsThreads)
+offsets_apply(const int32_t* __restrict__ counts, int64_t W, const int64_t* __restrict__ sums,
+              bool scanned, int32_t* __restrict__ offsets, const int32_t* __restrict__ err,
+              int64_t* __restrict__ status)
+{
+    __shared__ int64_t lds[kOffsThreads / kWave];
+    int64_t before;
+    if (scanned) {
+        before = sums[blockIdx.x];
+    } else {
+        int64_t part = 0;
+        for (int64_t i = threadIdx.x; i < (int64_t)blockIdx.x; i += kOffsThreads) part += sums[i];
+        (void)block_exclusive_scan<kOffsThreads>(part, lds, before);
+    }
+    const int64_t base = (int64_t)blockIdx.x * kOffsTile + (int64_t)threadIdx.x * kOffsPerThread;
+    int64_t v[kOffsPerThread];
+    int64_t s = 0;
+#pragma unroll
+    for (int i = 0; i < kOffsPerThread; ++i) {
+        v[i] = (base + i < W) ? counts[base + i] : 0;
+        s += v[i];
+    }
+    int64_t total;
+    int64_t ex = block_exclusive_scan<kOffsThreads>(s, lds, total) + before;
+#pragma unroll
+    for (int i = 0; i < kOffsPerThread; ++i) {
+        if (base + i < W) offsets[base + i] = (int32_t)ex;
+        ex += v[i];
+    }
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) {
+        offsets[W] = (int32_t)(before + total);
+        status[0] = *err;
+        status[1] = before + total;
+    }
+}
+
+// `sums` holds offsets_sum_elems(W) elements.
+static int64_t offsets_sum_elems(int64_t W) { return W > 0 ? ceil_div(W, kOffsTile) : 1; }
+
+static f3s_status counts_to_offsets(const int32_t* counts, int32_t* offsets, int64_t W,
+                                    int64_t* sums, const int32_t* err, int64_t* status,
+                                    hipStream_t stream)
+{
+    const int64_t nb = offsets_sum_elems(W);
+    hipLaunchKernelGGL(offsets_block_sums, dim3((unsigned)nb), dim3(kOffsThreads), 0, stream,
+                       counts, W, sums);
+    const bool scanned = nb > kOffsFusedBlocks;
+    if (scanned)
+        hipLaunchKernelGGL(offsets_scan_sums, dim3(1), dim3(kOffsThreads), 0, stream, sums, nb);
+    hipLaunchKernelGGL(offsets_apply, dim3((unsigned)nb), dim3(kOffsThreads), 0, stream, counts,
+                       W, sums, scanned, offsets, err, status);
+    F3S_HIP(hipGetLastError());
+    return F3S_OK;
+}
+
 // The fill pass's error bits and the tile count it was given (status[0..1]).
 __global__ void fill_status(const int32_t* __restrict__ window_offsets, int32_t W,
                             const int32_t* __restrict__ err, int64_t* __restrict__ status)
@@ -1197,7 +1295,7 @@ static f3s_status convert_scratch(StreamBuffer& buf, int32_t W, bool count, Conv
     const size_t hubs = sizeof(int4) * ((size_t)W + 1);
     const size_t sorted = count ? 0 : sizeof(int32_t) * ((size_t)W + 1);
     const size_t counts = count ? sizeof(int32_t) * (size_t)W : 0;
-    const size_t tmp = count ? sizeof(int64_t) * (size_t)scan_tmp_elems(W) : 0;
+    const size_t tmp = count ? sizeof(int64_t) * (size_t)offsets_sum_elems(W) : 0;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     F3S_TRY(buf.reserve(al(head) + al(hubs) + al(sorted) + al(counts) + al(tmp)));
     char* p = static_cast<char*>(buf.ptr);
@@ -1334,9 +1432,7 @@ static f3s_status convert_impl(const int32_t* row_ptr, const int32_t* col_idx, i
     if (count) {
         F3S_TRY(launch_pass<false>(row_ptr, col_idx, n, nnz, W, s.counts, nullptr, nullptr,
                                    nullptr, s.hl, nullptr, s.err, stream));
-        // T <= nnz <= INT32_MAX (a tile holds at least one edge): int32 offsets
-        F3S_TRY(exclusive_scan_i32_to_i32(s.counts, window_offsets, W, s.tmp, s.err, s.status,
-                                          stream));
+        F3S_TRY(counts_to_offsets(s.counts, window_offsets, W, s.tmp, s.err, s.status, stream));
     } else {
         F3S_TRY(launch_pass<true>(row_ptr, col_idx, n, nnz, W, nullptr, window_offsets,
                                   block_col, tile_mask, s.hl, s.hubs_sorted, s.err, stream));

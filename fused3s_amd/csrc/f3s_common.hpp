@@ -31,12 +31,6 @@ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t scan_tmp_elems(int64_t count);
 f3s_status exclusive_scan_i32_to_i64(const int32_t* in, int64_t* out, int64_t count,
                                      int64_t* tmp, hipStream_t stream);
-// The same into int32 (the caller knows the total fits), in two launches
-// while the count spans at most 2 M elements; given `status` (device), the
-// last workgroup also writes status[0] = *err and status[1] = the total.
-f3s_status exclusive_scan_i32_to_i32(const int32_t* in, int32_t* out, int64_t count,
-                                     int64_t* tmp, const int32_t* err, int64_t* status,
-                                     hipStream_t stream);
 
 // Each translation unit's code object is loaded onto the device at its
 // first kernel launch; these launch one empty kernel per unit (f3s_init).

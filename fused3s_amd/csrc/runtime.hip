@@ -375,68 +375,6 @@ scan_apply(const int32_t* __restrict__ in, int64_t count, const int64_t* __restr
     }
 }
 
-// scan_apply into int32 offsets.  With `scanned` false each workgroup adds
-// up the block sums before its own (no launch for the scan of the sums);
-// with it true they are already exclusive prefix sums (scan_sums_single).
-// The last workgroup writes out[count] (the total) and, given `status`,
-// status[0] = *err and status[1] = the total.
-__global__ void __launch_bounds__(kScanThreads)
-scan_apply_i32(const int32_t* __restrict__ in, int64_t count, const int64_t* __restrict__ sums,
-               bool scanned, int32_t* __restrict__ out, const int32_t* __restrict__ err,
-               int64_t* __restrict__ status)
-{
-    __shared__ int64_t lds[kScanThreads / kWave];
-    int64_t before;
-    if (scanned) {
-        before = sums[blockIdx.x];
-    } else {
-        int64_t part = 0;
-        for (int64_t i = threadIdx.x; i < (int64_t)blockIdx.x; i += kScanThreads) part += sums[i];
-        (void)block_exclusive_scan<kScanThreads>(part, lds, before);
-    }
-    const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanPerThread;
-    int64_t v[kScanPerThread];
-    int64_t s = 0;
-#pragma unroll
-    for (int i = 0; i < kScanPerThread; ++i) {
-        v[i] = (base + i < count) ? in[base + i] : 0;
-        s += v[i];
-    }
-    int64_t total;
-    int64_t ex = block_exclusive_scan<kScanThreads>(s, lds, total) + before;
-#pragma unroll
-    for (int i = 0; i < kScanPerThread; ++i) {
-        if (base + i < count) out[base + i] = (int32_t)ex;
-        ex += v[i];
-    }
-    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) {
-        out[count] = (int32_t)(before + total);
-        if (status) {
-            status[0] = *err;
-            status[1] = before + total;
-        }
-    }
-}
-
-f3s_status exclusive_scan_i32_to_i32(const int32_t* in, int32_t* out, int64_t count,
-                                     int64_t* tmp, const int32_t* err, int64_t* status,
-                                     hipStream_t stream)
-{
-    // up to kScanFusedBlocks workgroups, each adds up its predecessors' sums
-    constexpr int64_t kScanFusedBlocks = 1024;
-    const int64_t nb = count > 0 ? ceil_div(count, kScanTile) : 1;
-    hipLaunchKernelGGL(scan_block_sums, dim3((unsigned)nb), dim3(kScanThreads), 0, stream,
-                       in, count, tmp);
-    const bool scanned = nb > kScanFusedBlocks;
-    if (scanned)
-        hipLaunchKernelGGL(scan_sums_single, dim3(1), dim3(kScanThreads), 0, stream, tmp, nb,
-                           tmp + nb);
-    hipLaunchKernelGGL(scan_apply_i32, dim3((unsigned)nb), dim3(kScanThreads), 0, stream, in,
-                       count, tmp, scanned, out, err, status);
-    F3S_HIP(hipGetLastError());
-    return F3S_OK;
-}
-
 f3s_status exclusive_scan_i32_to_i64(const int32_t* in, int64_t* out, int64_t count,
                                      int64_t* tmp, hipStream_t stream)
 {

@@ -170,6 +170,33 @@ def test_converter_configs_small(gpu, cfg):
     check_converter(gpu, rp, ci)
 
 
+@pytest.mark.parametrize("n", [0, 37])
+def test_graph_without_edges(gpu, n):
+    """No node (W = 0) or no edge at all (T = 0): the converter's offsets are
+    all zero and T = 0 (converter.cu:15-44 gives the same), the window order
+    is the identity, and every pass leaves O = 0 (a node without neighbours
+    gets zeros, cpu_baseline.cpp:26-32; an empty window writes zeros)."""
+    rp = np.zeros(n + 1, np.int32)
+    ci = np.zeros(0, np.int32)
+    bsf = check_converter(gpu, rp, ci)
+    W = (n + 15) // 16
+    assert bsf.W == W and bsf.T == 0
+    fmt = gpu.convert_csr_to_block_sparse(n, rp, ci, verbose=False)
+    assert fmt.num_row_windows == W and len(fmt.block_col_indices) == 0
+    assert fmt.duplicate_entries == 0
+    assert np.array_equal(np.sort(gpu.generate_balanced_window_order(fmt)), np.arange(W))
+    order = gpu.window_order_device(bsf)
+    if W:
+        assert np.array_equal(order.numpy(), np.arange(W))
+    if n == 0:
+        return
+    P = Problem(gpu, rp, ci)
+    for masked in (True, False):
+        assert np.array_equal(P.run(masked=masked), np.zeros((n, 1, 64), np.float32))
+        assert np.array_equal(P.run(masked=masked, planned=True, compiled=masked),
+                              np.zeros((n, 1, 64), np.float32))
+
+
 @pytest.mark.parametrize("n,deg,seed", [(1, 0, 0), (2, 1, 1), (17, 3, 2), (100, 5, 3),
                                         (1000, 40, 4), (4099, 7, 5)])
 def test_converter_random(gpu, n, deg, seed):
