@@ -14,6 +14,12 @@ raises.
     o = graph.attention(q, k, v)                       # q/k/v [n, H, 64] fp16 -> fp32
     layer = GraphTransformerLayer(in_dim, heads=4).cuda().half()
     y = layer(x, graph)                                # x [n, in_dim] fp16
+
+The drop-in launch is also a registered torch operator, on the block-sparse
+form held in torch tensors (no plan, no state between calls):
+
+    offs, bcol, mask = to_block_sparse(row_ptr, col_idx)        # GPU converter
+    o = torch.ops.fused3s.attention_fwd(q, k, v, offs, bcol, mask, order, scale)
 """
 from __future__ import annotations
 
@@ -39,8 +45,11 @@ if len(_hip_runtimes()) > 1:
     raise ImportError("two HIP runtimes are loaded (" + ", ".join(sorted(_hip_runtimes())) +
                       "): import torch before the first fused3s_amd GPU call")
 
+import ctypes as C
+
+from . import _lib
 from .attention import Plan
-from .device import DeviceArray, Stream
+from .device import DeviceArray, Stream, check
 from .graph import DeviceBSF, DeviceCSR, convert_device, window_order_device
 
 HEAD_DIM = 64
@@ -143,3 +152,110 @@ class GraphTransformerLayer(torch.nn.Module):
         q, k, v = (qkv[:, i].contiguous() for i in range(3))
         o = graph.attention(q, k, v, scale=self.scale)
         return self.proj(o.view(n, self.heads * HEAD_DIM).to(self.proj.weight.dtype))
+
+
+# ------------------------------------------------------------------ operator
+
+def _cuda_i32(t, what: str) -> torch.Tensor:
+    t = torch.as_tensor(t)
+    if not t.is_cuda:
+        t = t.to("cuda")
+    if t.dtype != torch.int32:
+        raise ValueError(f"{what} must hold int32 values")
+    return t.contiguous()
+
+
+def to_block_sparse(row_ptr, col_idx, masks: bool = True):
+    """convert_csr_to_block_sparse (src/converter.cu:13-44) on the GPU into
+    torch tensors: (window_offsets int32 [W + 1], block_col_indices int32
+    [T], tile_mask int16 [T, 16] -- bit c of row r of a tile set iff that
+    edge exists -- or None).  Two calls of f3s_convert_csr_to_bsf on torch's
+    current stream: the count (one host round trip for T), then the fill."""
+    rp = _cuda_i32(row_ptr, "row_ptr")
+    ci = _cuda_i32(col_idx, "col_idx")
+    n = rp.numel() - 1
+    if n < 0:
+        raise ValueError("row_ptr must hold n + 1 entries")
+    W = (n + 15) // 16
+    lib = _lib.hip()
+    s = torch.cuda.current_stream().cuda_stream
+    offs = torch.empty(W + 1, dtype=torch.int32, device=rp.device)
+    T = C.c_int64(0)
+    cptr = ci.data_ptr() if ci.numel() else None
+    check(lib.f3s_convert_csr_to_bsf(rp.data_ptr(), cptr, n, ci.numel(), offs.data_ptr(), None,
+                                     None, C.byref(T), s), "f3s_convert_csr_to_bsf(count)")
+    t = int(T.value)
+    # at least one element each, so the fill call gets real pointers
+    bcol = torch.empty(max(t, 1), dtype=torch.int32, device=rp.device)
+    mask = torch.empty((max(t, 1), 16), dtype=torch.int16, device=rp.device) if masks else None
+    T2 = C.c_int64(0)
+    check(lib.f3s_convert_csr_to_bsf(rp.data_ptr(), cptr, n, ci.numel(), offs.data_ptr(),
+                                     bcol.data_ptr(), mask.data_ptr() if masks else None,
+                                     C.byref(T2), s), "f3s_convert_csr_to_bsf(fill)")
+    return offs, bcol[:t], (mask[:t] if masks else None)
+
+
+def _check_operands(q, k, v, window_offsets, block_col, tile_mask, window_order):
+    if q.dim() != 3 or q.shape[2] != HEAD_DIM:
+        raise ValueError(f"q must be [n, H, {HEAD_DIM}]")
+    n, H = q.shape[0], q.shape[1]
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.dtype != torch.float16 or not t.is_cuda or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float16 CUDA tensor")
+        if tuple(t.shape) != (n, H, HEAD_DIM):
+            raise ValueError(f"{name} must have shape {(n, H, HEAD_DIM)}, got {tuple(t.shape)}")
+    W = (n + 15) // 16
+    for name, t, shape in (("window_offsets", window_offsets, (W + 1,)),
+                           ("block_col", block_col, None),
+                           ("window_order", window_order, (W,))):
+        if t is None:
+            if name != "window_order":
+                raise ValueError(f"{name} is required")
+            continue
+        if t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous() or t.dim() != 1:
+            raise ValueError(f"{name} must be a contiguous 1-d int32 CUDA tensor")
+        if shape is not None and tuple(t.shape) != shape:
+            raise ValueError(f"{name} must have shape {shape}, got {tuple(t.shape)}")
+    if tile_mask is not None:
+        if (tile_mask.dtype not in (torch.int16, torch.uint16) or not tile_mask.is_cuda
+                or not tile_mask.is_contiguous()
+                or tuple(tile_mask.shape) != (block_col.shape[0], 16)):
+            raise ValueError("tile_mask must be a contiguous [T, 16] int16 CUDA tensor")
+    return n, H, W
+
+
+@torch.library.custom_op("fused3s::attention_fwd", mutates_args=())
+def attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                  window_offsets: torch.Tensor, block_col: torch.Tensor,
+                  tile_mask: torch.Tensor | None, window_order: torch.Tensor | None,
+                  scale: float = 1.0) -> torch.Tensor:
+    """f3s_attention_fwd (the reference's launch, tests/test_fused_3s_v2.cu:
+    124-131, every window whole) on torch tensors and torch's current
+    stream: q/k/v [n, H, 64] float16, the block-sparse form of
+    to_block_sparse, window_order int32 [W] or None (natural order); a
+    tile_mask gives the masked (edge-exact) semantics, None the reference's
+    tile-dense one.  Returns O [n, H, 64] float32."""
+    if q.requires_grad or k.requires_grad or v.requires_grad:
+        raise RuntimeError("the fused pass is forward-only (no autograd)")
+    n, H, W = _check_operands(q, k, v, window_offsets, block_col, tile_mask, window_order)
+    out = torch.empty((n, H, HEAD_DIM), dtype=torch.float32, device=q.device)
+    if n == 0:
+        return out
+    s = torch.cuda.current_stream(q.device).cuda_stream
+    # an empty block_col tensor may have no storage: the C-ABI wants a pointer
+    # whenever W > 0, and with T = 0 no tile is read through it
+    bptr = block_col.data_ptr() or window_offsets.data_ptr()
+    mptr = None
+    if tile_mask is not None:
+        mptr = tile_mask.data_ptr() or out.data_ptr()
+    check(_lib.hip().f3s_attention_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                       window_offsets.data_ptr(), bptr, mptr,
+                                       window_order.data_ptr() if window_order is not None
+                                       else None, W, n, HEAD_DIM, H, float(scale), s),
+          "f3s_attention_fwd")
+    return out
+
+
+@attention_fwd.register_fake
+def _attention_fwd_fake(q, k, v, window_offsets, block_col, tile_mask, window_order, scale=1.0):
+    return torch.empty(q.shape, dtype=torch.float32, device=q.device)

@@ -109,3 +109,45 @@ def test_rejects_grad_and_bad_inputs(torch_ops):
         graph.attention(q.float(), q, q)
     with pytest.raises(ValueError, match="shape"):
         graph.attention(q[:32], q, q)
+
+
+@pytest.mark.parametrize("H", [1, 3])
+def test_registered_operator(torch_ops, H):
+    """torch.ops.fused3s.attention_fwd (the drop-in launch as a torch
+    operator) on the block-sparse form of to_block_sparse: the converter's
+    tensors equal the oracle converter's bit for bit, both semantics meet
+    the oracle in the descending and natural orders, the operator's schema
+    and fake (meta) implementation pass torch.library.opcheck, and bad
+    operands raise."""
+    import torch
+    rp, ci = random_csr(1500, 9, 24)
+    n = len(rp) - 1
+    offs, bcol, mask = torch_ops.to_block_sparse(torch.from_numpy(rp), torch.from_numpy(ci))
+    w_offs, w_bcol, w_mask = orc.convert(n, rp, ci)
+    assert np.array_equal(offs.cpu().numpy(), w_offs)
+    assert np.array_equal(bcol.cpu().numpy(), w_bcol)
+    assert np.array_equal(mask.cpu().numpy().view(np.uint16), w_mask)
+    order = torch.from_numpy(orc.window_order(w_offs)).cuda()
+    gen = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(n, H, 64, generator=gen).half().cuda() for _ in range(3))
+    f = lambda t: t.float().cpu().numpy()
+    want_m = orc.masked_attention(n, 64, H, f(q), f(k), f(v), rp, ci, 0.25)
+    want_d = orc.tile_dense_attention(n, 64, H, f(q), f(k), f(v), w_offs, w_bcol, 0.25, fast=True)
+    op = torch.ops.fused3s.attention_fwd
+    for o_arg in (order, None):
+        got_m = op(q, k, v, offs, bcol, mask, o_arg, 0.25)
+        got_d = op(q, k, v, offs, bcol, None, o_arg, 0.25)
+        torch.cuda.synchronize()
+        tag = "descending" if o_arg is not None else "natural"
+        close(got_m.cpu().numpy(), want_m, f"operator masked {tag} H={H}")
+        close(got_d.cpu().numpy(), want_d, f"operator tile-dense {tag} H={H}")
+    torch.library.opcheck(op, (q, k, v, offs, bcol, mask, order, 0.25),
+                          test_utils=("test_schema", "test_faketensor"))
+    with pytest.raises(RuntimeError, match="forward-only"):
+        op(q.clone().requires_grad_(), k, v, offs, bcol, mask, order, 0.25)
+    with pytest.raises(ValueError, match="float16"):
+        op(q.float(), k, v, offs, bcol, mask, order, 0.25)
+    with pytest.raises(ValueError, match="window_offsets"):
+        op(q, k, v, offs[:-1], bcol, mask, order, 0.25)
+    with pytest.raises(ValueError, match="tile_mask"):
+        op(q, k, v, offs, bcol, mask[:-1], order, 0.25)
