@@ -496,7 +496,7 @@ __host__ __device__ inline LightLayout light_layout(int32_t W, bool fill)
     l.off_base = o;
     if (fill) o = align16(o + 2u * (uint32_t)l.words);
     l.off_sum = o;
-    if (fill) o = align16(o + 4u * (uint32_t)l.sums);
+    if (fill) o = align16(o + 8u * (uint32_t)l.sums);   // summary, then tiles per summary word
     l.off_masks = o;
     if (fill) o = align16(o + 4u * kMaskTiles * 8);
     l.off_tcol = o;
@@ -513,6 +513,7 @@ struct LightLds {
     uint32_t* bits;     // [words] block columns of the window
     uint16_t* base;     // [words] tiles before each word (fill)
     uint32_t* summary;  // [sums] non-empty bitmap words (fill)
+    int32_t* scnt;      // [sums] tiles under each summary word (fill)
     uint32_t* masks;    // [kMaskTiles * 8] staged row masks, two rows per word (fill)
     int32_t* tcol;      // [kMaskTiles] staged block columns (fill)
     int32_t* meta;      // [kMetaSlots][kMetaInts] window descriptions (ring)
@@ -528,6 +529,7 @@ __device__ __forceinline__ LightLds light_lds(const LightLayout& lay)
     L.bits = reinterpret_cast<uint32_t*>(conv_lds);
     L.base = reinterpret_cast<uint16_t*>(conv_lds + lay.off_base);
     L.summary = reinterpret_cast<uint32_t*>(conv_lds + lay.off_sum);
+    L.scnt = reinterpret_cast<int32_t*>(L.summary + lay.sums);
     L.masks = reinterpret_cast<uint32_t*>(conv_lds + lay.off_masks);
     L.tcol = reinterpret_cast<int32_t*>(conv_lds + lay.off_tcol);
     L.meta = reinterpret_cast<int32_t*>(conv_lds + lay.off_meta);
@@ -704,6 +706,7 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
         const uint32_t old = atomicOr(&L.bits[wi], bit);
         if (FILL) {
             if (old == 0u) atomicOr(&L.summary[wi >> 5], 1u << (wi & 31));
+            if ((old & bit) == 0u) atomicAdd(&L.scnt[wi >> 5], 1);   // a new tile
         } else {
             fresh += (old & bit) == 0u;
         }
@@ -723,16 +726,16 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
         if (wid == 0) {
             const int spl = (L.sums + kWave - 1) / kWave;
             const int s0 = min(L.sums, lane * spl), s1 = min(L.sums, s0 + spl);
+            // the tiles under each summary word were counted while marking
             int32_t own = 0;
-            for (int sw = s0; sw < s1; ++sw)
-                for (uint32_t t = L.summary[sw]; t; t &= t - 1u)
-                    own += __popc(L.bits[sw * 32 + __builtin_ctz(t)]);
+            for (int sw = s0; sw < s1; ++sw) own += L.scnt[sw];
             const int32_t incl = wave_inclusive_scan(own);
             int32_t t0 = incl - own;
             for (int sw = s0; sw < s1; ++sw) {
                 uint32_t t = L.summary[sw];
                 if (!t) continue;
                 L.summary[sw] = 0u;
+                L.scnt[sw] = 0;
                 for (; t; t &= t - 1u) {
                     const int wi = sw * 32 + __builtin_ctz(t);
                     L.base[wi] = (uint16_t)t0;
@@ -809,7 +812,7 @@ convert_light(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ c
     if constexpr (FILL) {
         for (int g = tid; g < kMaskTiles * 2; g += kConvThreads)
             *reinterpret_cast<uint4*>(&L.masks[4 * g]) = make_uint4(0u, 0u, 0u, 0u);
-        for (int g = tid; g < L.sums; g += kConvThreads) L.summary[g] = 0u;
+        for (int g = tid; g < 2 * L.sums; g += kConvThreads) L.summary[g] = 0u;   // + scnt
     }
     if (tid < kMiscInts) L.cnt[tid] = 0;
     const int32_t total_tiles = FILL ? window_offsets[W] : 0;
