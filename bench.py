@@ -135,29 +135,32 @@ def read_profile(path: Path, key: str) -> float | None:
     return None
 
 
-def convert_phases_ms(csr, bsf, stream) -> float:
+def convert_phases_ms(csr, bsf, stream, reps: int = 5) -> float:
     """GPU time of f3s_convert_csr_to_bsf's count call plus its fill call into
     the outputs of an earlier conversion of the same CSR (HIP events on the
-    launch stream around each call)."""
+    launch stream around each call); the median of `reps` conversions."""
     import fused3s_amd as f3s
     from fused3s_amd import _lib
     from fused3s_amd.device import check
     lib = _lib.hip()
-    e = [f3s.Event() for _ in range(4)]
     T = C.c_int64(0)
-    e[0].record(stream)
-    check(lib.f3s_convert_csr_to_bsf(csr.row_ptr.ptr, csr.col_idx.ptr, csr.n, csr.nnz,
-                                     bsf.window_offsets.ptr, None, None, C.byref(T),
-                                     stream.handle), "convert(count)")
-    e[1].record(stream)
-    e[2].record(stream)
-    check(lib.f3s_convert_csr_to_bsf(csr.row_ptr.ptr, csr.col_idx.ptr, csr.n, csr.nnz,
-                                     bsf.window_offsets.ptr, bsf.block_col.ptr,
-                                     bsf.tile_mask.ptr, C.byref(T), stream.handle),
-          "convert(fill)")
-    e[3].record(stream)
-    f3s.synchronize()
-    return e[0].elapsed_ms(e[1]) + e[2].elapsed_ms(e[3])
+    times = []
+    for _ in range(reps):
+        e = [f3s.Event() for _ in range(4)]
+        e[0].record(stream)
+        check(lib.f3s_convert_csr_to_bsf(csr.row_ptr.ptr, csr.col_idx.ptr, csr.n, csr.nnz,
+                                         bsf.window_offsets.ptr, None, None, C.byref(T),
+                                         stream.handle), "convert(count)")
+        e[1].record(stream)
+        e[2].record(stream)
+        check(lib.f3s_convert_csr_to_bsf(csr.row_ptr.ptr, csr.col_idx.ptr, csr.n, csr.nnz,
+                                         bsf.window_offsets.ptr, bsf.block_col.ptr,
+                                         bsf.tile_mask.ptr, C.byref(T), stream.handle),
+              "convert(fill)")
+        e[3].record(stream)
+        f3s.synchronize()
+        times.append(e[0].elapsed_ms(e[1]) + e[2].elapsed_ms(e[3]))
+    return float(np.median(times))
 
 
 def time_passes(f3s, one_pass, stream, reps: int) -> np.ndarray:
