@@ -157,11 +157,17 @@ class GraphTransformerLayer(torch.nn.Module):
 # ------------------------------------------------------------------ operator
 
 def _cuda_i32(t, what: str) -> torch.Tensor:
+    """An int32 CUDA copy (or view) of an integer array; int64 input (the
+    usual index type of torch graph code) is narrowed after a range check."""
     t = torch.as_tensor(t)
+    if t.dtype == torch.int64:
+        if t.numel() and (int(t.min()) < -2**31 or int(t.max()) >= 2**31):
+            raise ValueError(f"{what} holds values outside the int32 range")
+        t = t.to(torch.int32)
+    elif t.dtype != torch.int32:
+        raise ValueError(f"{what} must hold int32 (or int64) values")
     if not t.is_cuda:
         t = t.to("cuda")
-    if t.dtype != torch.int32:
-        raise ValueError(f"{what} must hold int32 values")
     return t.contiguous()
 
 

@@ -122,7 +122,8 @@ def test_registered_operator(torch_ops, H):
     import torch
     rp, ci = random_csr(1500, 9, 24)
     n = len(rp) - 1
-    offs, bcol, mask = torch_ops.to_block_sparse(torch.from_numpy(rp), torch.from_numpy(ci))
+    offs, bcol, mask = torch_ops.to_block_sparse(torch.from_numpy(rp),
+                                                 torch.from_numpy(ci).long())   # int64 narrowed
     w_offs, w_bcol, w_mask = orc.convert(n, rp, ci)
     assert np.array_equal(offs.cpu().numpy(), w_offs)
     assert np.array_equal(bcol.cpu().numpy(), w_bcol)
