@@ -13,8 +13,9 @@
 //     to the graph (up to 4.2 M nodes).  Every edge ORs its block column's
 //     bit into the bitmap; a bit set for the first time is a new tile, so
 //     the count pass needs no scan.  The fill pass marks non-empty bitmap
-//     words in a summary, turns it into word bases (a tile's output rank is
-//     the base of its word plus the set bits below it), stages the row masks
+//     words in a summary and counts the new tiles under each summary word,
+//     turns those into word bases (a tile's output rank is the base of its
+//     word plus the set bits below it), stages the row masks
 //     and block columns of up to kMaskTiles tiles in LDS and streams them
 //     out in coalesced stores.  Each workgroup keeps the loads of its next
 //     window in flight while it works on the current one, and its barriers
@@ -433,10 +434,12 @@ convert_hubs(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ co
 // graph) stays clear between windows: each edge clears its own word after
 // use.  Per window:
 //   mark   every edge ORs its block column's bit into the bitmap; a bit set
-//          for the first time is a new tile (count); the first setter of a
-//          word also marks the word in the summary (fill);
-//   base   (fill) wave 0 turns the summary into word bases: a tile's output
-//          rank is the base of its word plus the set bits below it;
+//          for the first time is a new tile (count; filling, it adds one to
+//          its summary word's tile count); the first setter of a word also
+//          marks the word in the summary (fill);
+//   base   (fill) wave 0 scans the summary words' tile counts and turns the
+//          summary into word bases: a tile's output rank is the base of its
+//          word plus the set bits below it;
 //   stage  (fill) every edge ORs its bit into its tile's staged row masks and
 //          records the tile's block column, kMaskTiles tiles per round; each
 //          thread then streams out (and re-zeroes) the tiles it owns, so
