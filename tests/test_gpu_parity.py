@@ -285,6 +285,25 @@ def test_converter_bitmap_limit(gpu, n):
     check_converter(gpu, rp.astype(np.int32), ci)
 
 
+def test_converter_offsets_past_2m_windows(gpu):
+    # 34,000,000 nodes = 2,125,000 windows: more than 1,024 blocks of 2,048
+    # window counts, so the count call scans the block sums in a launch of
+    # their own before writing the offsets (below that, each block adds up
+    # its predecessors' sums itself); a few thousand edges, spread over the
+    # whole column range, with repeats and a hub window.
+    n = 34_000_000
+    r = rng(13)
+    rows = np.sort(r.integers(0, n, 6000))
+    rows = np.concatenate([rows, np.full(1500, 16 * 1_000_003)])   # one hub window
+    rows.sort()
+    deg = np.bincount(rows, minlength=n)
+    rp = np.zeros(n + 1, np.int64)
+    rp[1:] = np.cumsum(deg)
+    ci = r.integers(0, n, int(rp[-1])).astype(np.int32)
+    ci[::7] = ci[0]                                             # repeated columns
+    check_converter(gpu, rp.astype(np.int32), ci)
+
+
 def test_converter_unsorted_and_empty_windows(gpu):
     n = 64
     rows = {0: [63, 1, 17, 1, 63], 5: [0, 0], 48: [47, 3, 62, 16], 63: [63]}
