@@ -982,6 +982,7 @@ count_waves(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col
             int fresh = 0;
 #pragma unroll
             for (int j = 0; j < kWaveCountEPL; ++j) {
+                if (kWave * j >= d.E) break;   // wave-uniform: no edge in this slot
                 const int32_t c = col[j];
                 if (lane + kWave * j < d.E) {
                     if (c < 0 || c >= n) {
@@ -996,6 +997,7 @@ count_waves(const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col
             F3S_WAVE_LDS_SYNC();   // every mark is done before the clears
 #pragma unroll
             for (int j = 0; j < kWaveCountEPL; ++j) {
+                if (kWave * j >= d.E) break;
                 const int32_t c = col[j];
                 if (lane + kWave * j < d.E && c >= 0 && c < n) bits[c >> 9] = 0u;
             }
