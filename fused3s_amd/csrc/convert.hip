@@ -947,8 +947,10 @@ __device__ __forceinline__ void wave_issue_cols(const WaveWin& d,
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int32_t*>(col_idx) + (E > 0 ? d.e0 : 0), (short)0, 4 * E, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < kWaveCountEPL; ++j)
+    for (int j = 0; j < kWaveCountEPL; ++j) {
+        if (kWave * j >= E) break;   // wave-uniform: the window has no edge here
         col[j] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * (lane + kWave * j), 0, 0);
+    }
 }
 
 __global__ void __launch_bounds__(kWaveCountWaves * kWave)
