@@ -685,10 +685,14 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
         return;
     }
 
+    // edge slots this wave uses: its lane 0 holds the longest run of the
+    // wave (runs are dealt in thread order); the loops below stop there
+    const int wcnt = __builtin_amdgcn_readfirstlane(cnt);
     // absent (j >= cnt) and invalid columns become -1; an invalid column
     // (outside [0, n)) is reported and left out
 #pragma unroll
     for (int j = 0; j < kLightEPT; ++j) {
+        if (j >= wcnt) break;
         const int32_t c = col[j];
         const bool present = j < cnt;
         const bool ok = present && c >= 0 && c < n;
@@ -702,6 +706,7 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
     int32_t fresh = 0;
 #pragma unroll
     for (int j = 0; j < kLightEPT; ++j) {
+        if (j >= wcnt) break;
         const int32_t c = col[j];
         if (c < 0) continue;
         const int32_t wi = c >> 9;
@@ -755,6 +760,7 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
                 if (ms > 0) lds_barrier();   // the previous round's tiles are re-zeroed
 #pragma unroll
                 for (int j = 0; j < kLightEPT; ++j) {
+                    if (j >= wcnt) break;
                     const int32_t c = col[j];
                     if (c < 0) continue;
                     const int32_t wi = c >> 9;
@@ -784,8 +790,10 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
     }
     // ---- clear (every reader of the bitmap is past B1, B2 or B3) ----
 #pragma unroll
-    for (int j = 0; j < kLightEPT; ++j)
+    for (int j = 0; j < kLightEPT; ++j) {
+        if (j >= wcnt) break;
         if (col[j] >= 0) L.bits[col[j] >> 9] = 0u;
+    }
     lds_barrier();   // B4: bitmap and staged masks clear for the next window
     if (tid == 0) {
         if (FILL) {
