@@ -634,14 +634,18 @@ __device__ __forceinline__ void issue_edges(const LightLds& L, int slot,
     const int per = (m.E + kConvThreads - 1) / kConvThreads;
     const int i0 = min(m.E, (int)threadIdx.x * per), i1 = min(m.E, i0 + per);
     cnt = i1 - i0;
+    const int wcnt = __builtin_amdgcn_readfirstlane(cnt);   // the wave's longest run
 #pragma unroll
-    for (int j = 0; j < kLightEPT; ++j)
+    for (int j = 0; j < kLightEPT; ++j) {
+        if (j >= wcnt) break;
         if (j < cnt) col[j] = col_idx[m.e0 + i0 + j];
+    }
     if (FILL && cnt > 0) {
         const int32_t* rp = L.meta + slot * kMetaInts;
         int r = row_of_edge(rp, m.nrows, m.e0 + i0);
 #pragma unroll
         for (int j = 0; j < kLightEPT; ++j) {
+            if (j >= wcnt) break;
             const int32_t e = m.e0 + i0 + j;
             while (r + 1 < m.nrows && e >= rp[r + 1]) ++r;
             rows |= (uint32_t)r << (4 * j);
