@@ -161,6 +161,9 @@ convert_one_window(ConvLds<FILL, NT>& L, int32_t w, const int32_t* __restrict__ 
     const int per = (E + NT - 1) / NT;
     const int i0 = min(E, tid * per), i1 = min(E, i0 + per);
     const bool in_regs = E <= kRegEdgesNT;   // i.e. per <= kEPT
+    // the wave's longest run (its lane 0's: runs are dealt in thread order);
+    // the register loops stop there
+    const int wcnt = __builtin_amdgcn_readfirstlane(i1 - i0);
 
     // Visits the run's valid edges (column c, row r) in order.
     int32_t col[kEPT];
@@ -168,8 +171,10 @@ convert_one_window(ConvLds<FILL, NT>& L, int32_t w, const int32_t* __restrict__ 
     auto for_each_edge = [&](auto&& fn) {
         if (in_regs) {
 #pragma unroll
-            for (int j = 0; j < kEPT; ++j)
+            for (int j = 0; j < kEPT; ++j) {
+                if (j >= wcnt) break;
                 if (col[j] >= 0) fn(col[j], (int)((rows >> (4 * j)) & 15u));
+            }
         } else {
             // kHubBatch loads in flight per thread, then their edges in order
             int r = i0 < i1 ? row_of_edge(L.rp, nrows, e0 + i0) : 0;
@@ -203,6 +208,7 @@ convert_one_window(ConvLds<FILL, NT>& L, int32_t w, const int32_t* __restrict__ 
         if (in_regs) {
 #pragma unroll
             for (int j = 0; j < kEPT; ++j) {
+                if (j >= wcnt) break;
                 const int i = i0 + j;
                 int32_t c = -1;
                 if (i < i1) {
@@ -1093,11 +1099,13 @@ count_hubs(const int32_t* __restrict__ col_idx, int32_t n, int64_t nnz, int32_t 
             int32_t col[kHubCountEPT];
 #pragma unroll
             for (int j = 0; j < kHubCountEPT; ++j) {
+                if (c0 + NT * j >= E) break;   // uniform: no edge of the chunk here
                 const int64_t e = c0 + tid + NT * j;
                 col[j] = e < E ? col_idx[e0 + e] : 0;
             }
 #pragma unroll
             for (int j = 0; j < kHubCountEPT; ++j) {
+                if (c0 + NT * j >= E) break;
                 const int64_t e = c0 + tid + NT * j;
                 if (e >= E) continue;
                 const int32_t c = col[j];
