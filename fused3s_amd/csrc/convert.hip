@@ -161,9 +161,6 @@ convert_one_window(ConvLds<FILL, NT>& L, int32_t w, const int32_t* __restrict__ 
     const int per = (E + NT - 1) / NT;
     const int i0 = min(E, tid * per), i1 = min(E, i0 + per);
     const bool in_regs = E <= kRegEdgesNT;   // i.e. per <= kEPT
-    // the wave's longest run (its lane 0's: runs are dealt in thread order);
-    // the register loops stop there
-    const int wcnt = __builtin_amdgcn_readfirstlane(i1 - i0);
 
     // Visits the run's valid edges (column c, row r) in order.
     int32_t col[kEPT];
@@ -171,10 +168,8 @@ convert_one_window(ConvLds<FILL, NT>& L, int32_t w, const int32_t* __restrict__ 
     auto for_each_edge = [&](auto&& fn) {
         if (in_regs) {
 #pragma unroll
-            for (int j = 0; j < kEPT; ++j) {
-                if (j >= wcnt) break;
+            for (int j = 0; j < kEPT; ++j)
                 if (col[j] >= 0) fn(col[j], (int)((rows >> (4 * j)) & 15u));
-            }
         } else {
             // kHubBatch loads in flight per thread, then their edges in order
             int r = i0 < i1 ? row_of_edge(L.rp, nrows, e0 + i0) : 0;
@@ -208,7 +203,6 @@ convert_one_window(ConvLds<FILL, NT>& L, int32_t w, const int32_t* __restrict__ 
         if (in_regs) {
 #pragma unroll
             for (int j = 0; j < kEPT; ++j) {
-                if (j >= wcnt) break;
                 const int i = i0 + j;
                 int32_t c = -1;
                 if (i < i1) {
@@ -640,18 +634,14 @@ __device__ __forceinline__ void issue_edges(const LightLds& L, int slot,
     const int per = (m.E + kConvThreads - 1) / kConvThreads;
     const int i0 = min(m.E, (int)threadIdx.x * per), i1 = min(m.E, i0 + per);
     cnt = i1 - i0;
-    const int wcnt = __builtin_amdgcn_readfirstlane(cnt);   // the wave's longest run
 #pragma unroll
-    for (int j = 0; j < kLightEPT; ++j) {
-        if (j >= wcnt) break;
+    for (int j = 0; j < kLightEPT; ++j)
         if (j < cnt) col[j] = col_idx[m.e0 + i0 + j];
-    }
     if (FILL && cnt > 0) {
         const int32_t* rp = L.meta + slot * kMetaInts;
         int r = row_of_edge(rp, m.nrows, m.e0 + i0);
 #pragma unroll
         for (int j = 0; j < kLightEPT; ++j) {
-            if (j >= wcnt) break;
             const int32_t e = m.e0 + i0 + j;
             while (r + 1 < m.nrows && e >= rp[r + 1]) ++r;
             rows |= (uint32_t)r << (4 * j);
@@ -695,14 +685,10 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
         return;
     }
 
-    // edge slots this wave uses: its lane 0 holds the longest run of the
-    // wave (runs are dealt in thread order); the loops below stop there
-    const int wcnt = __builtin_amdgcn_readfirstlane(cnt);
     // absent (j >= cnt) and invalid columns become -1; an invalid column
     // (outside [0, n)) is reported and left out
 #pragma unroll
     for (int j = 0; j < kLightEPT; ++j) {
-        if (j >= wcnt) break;
         const int32_t c = col[j];
         const bool present = j < cnt;
         const bool ok = present && c >= 0 && c < n;
@@ -716,7 +702,6 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
     int32_t fresh = 0;
 #pragma unroll
     for (int j = 0; j < kLightEPT; ++j) {
-        if (j >= wcnt) break;
         const int32_t c = col[j];
         if (c < 0) continue;
         const int32_t wi = c >> 9;
@@ -770,7 +755,6 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
                 if (ms > 0) lds_barrier();   // the previous round's tiles are re-zeroed
 #pragma unroll
                 for (int j = 0; j < kLightEPT; ++j) {
-                    if (j >= wcnt) break;
                     const int32_t c = col[j];
                     if (c < 0) continue;
                     const int32_t wi = c >> 9;
@@ -800,10 +784,8 @@ __device__ __forceinline__ void light_window(const LightLds& L, int slot, int32_
     }
     // ---- clear (every reader of the bitmap is past B1, B2 or B3) ----
 #pragma unroll
-    for (int j = 0; j < kLightEPT; ++j) {
-        if (j >= wcnt) break;
+    for (int j = 0; j < kLightEPT; ++j)
         if (col[j] >= 0) L.bits[col[j] >> 9] = 0u;
-    }
     lds_barrier();   // B4: bitmap and staged masks clear for the next window
     if (tid == 0) {
         if (FILL) {
@@ -1099,13 +1081,11 @@ count_hubs(const int32_t* __restrict__ col_idx, int32_t n, int64_t nnz, int32_t 
             int32_t col[kHubCountEPT];
 #pragma unroll
             for (int j = 0; j < kHubCountEPT; ++j) {
-                if (c0 + NT * j >= E) break;   // uniform: no edge of the chunk here
                 const int64_t e = c0 + tid + NT * j;
                 col[j] = e < E ? col_idx[e0 + e] : 0;
             }
 #pragma unroll
             for (int j = 0; j < kHubCountEPT; ++j) {
-                if (c0 + NT * j >= E) break;
                 const int64_t e = c0 + tid + NT * j;
                 if (e >= E) continue;
                 const int32_t c = col[j];
